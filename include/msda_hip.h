@@ -1,0 +1,117 @@
+/*
+ * msda_hip.h - C ABI of the MI355X (gfx950) multi-scale deformable attention
+ * operator.
+ *
+ * The library (libmsda_hip.so) is the drop-in replacement for the two device
+ * launches of the reference operator roulbac/msda-triton:
+ *
+ *   msda_forward   replaces the launch of `_msda_forward_kernel`
+ *                  (src/msda_triton/ops.py:46-52, kernel at
+ *                  src/msda_triton/kernels.py:58-163)
+ *   msda_backward  replaces the zero-fill, the launch of
+ *                  `_msda_backward_kernel` and the accumulator cast
+ *                  (src/msda_triton/ops.py:76-92, kernel at
+ *                  src/msda_triton/kernels.py:166-291)
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers to C-contiguous arrays.
+ *   - value                (B, S, M, D)        dtype
+ *     spatial_shapes       (L, 2) int64        (H_l, W_l), on the device
+ *     level_start_index    (L,)   int64        offset of level l along S, on the device
+ *     sampling_locations   (B, Q, M, L, K, 2)  dtype, normalised (x, y)
+ *     attention_weights    (B, Q, M, L, K)     dtype
+ *     output / grad_output (B, Q, M, D)        dtype
+ *   - Bilinear sampling follows grid_sample(align_corners=False,
+ *     padding_mode="zeros"): x = loc_x * W_l - 0.5, y = loc_y * H_l - 0.5,
+ *     corners outside [0, W_l) x [0, H_l) contribute zero.
+ *   - Arithmetic is fp32 for every storage dtype; results are rounded once to
+ *     the storage dtype.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream).
+ *     No entry point synchronises, allocates device memory or keeps state
+ *     between calls; all of them may be captured into a hipGraph.
+ *   - The return value is MSDA_OK or one of the MSDA_ERR_* codes below; the
+ *     device buffers are untouched when an argument error is returned.
+ */
+#ifndef MSDA_HIP_H_
+#define MSDA_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Storage dtype codes. */
+#define MSDA_DTYPE_F32 0
+#define MSDA_DTYPE_F16 1
+#define MSDA_DTYPE_BF16 2
+
+/* Return codes. */
+#define MSDA_OK 0
+#define MSDA_ERR_INVALID_ARGUMENT 1 /* negative size, NULL pointer for a non-empty array */
+#define MSDA_ERR_UNSUPPORTED_DTYPE 2
+#define MSDA_ERR_UNSUPPORTED_SHAPE 3 /* L > MSDA_MAX_LEVELS, D*elem > 1024 bytes, S >= 2^31 */
+#define MSDA_ERR_LAUNCH 4            /* hipGetLastError() after a launch */
+
+#define MSDA_MAX_LEVELS 64
+
+/*
+ * Forward: output[b,q,m,:] = sum_{l,k} A[b,q,m,l,k] *
+ *          bilinear(value[b, level l, m, :], sampling_locations[b,q,m,l,k]).
+ *
+ * Replaces src/msda_triton/ops.py:46-52 (allocation of `out` stays with the
+ * caller, as there) and the kernel src/msda_triton/kernels.py:58-163.
+ * batch..num_points are B, S, M, D, Q, L, K.  B*Q == 0 launches nothing.
+ */
+int msda_forward(const void* value, const int64_t* spatial_shapes,
+                 const int64_t* level_start_index, const void* sampling_locations,
+                 const void* attention_weights, void* output, int64_t batch,
+                 int64_t num_keys, int64_t num_heads, int64_t head_dim,
+                 int64_t num_queries, int64_t num_levels, int64_t num_points,
+                 int dtype, void* stream);
+
+/*
+ * Backward: the three analytic gradients of msda_forward.
+ *
+ * Replaces src/msda_triton/ops.py:76-92 and the kernel
+ * src/msda_triton/kernels.py:166-291.
+ *   grad_value              (B, S, M, D) dtype, written in full (the library
+ *                           zero-fills it on `stream`; the caller need not).
+ *   grad_value_accum        NULL: grad_value is accumulated in place with the
+ *                           dtype's own atomics (fp32 add, packed fp16/bf16
+ *                           add).  Non-NULL: an fp32 scratch array of B*S*M*D
+ *                           floats; gradients are accumulated there with fp32
+ *                           atomics and rounded once into grad_value.  This
+ *                           is the reference's `fp32_grad_accum=True`
+ *                           (src/msda_triton/ops.py:76-77,91-92).  For
+ *                           dtype == MSDA_DTYPE_F32 it may alias grad_value.
+ *   grad_sampling_locations (B, Q, M, L, K, 2) dtype, written in full.
+ *   grad_attention_weights  (B, Q, M, L, K)    dtype, written in full.
+ * grad_value is accumulated with atomics, so it is not bitwise
+ * deterministic; the other two gradients are.
+ */
+int msda_backward(const void* value, const int64_t* spatial_shapes,
+                  const int64_t* level_start_index, const void* sampling_locations,
+                  const void* attention_weights, const void* grad_output,
+                  void* grad_value, float* grad_value_accum,
+                  void* grad_sampling_locations, void* grad_attention_weights,
+                  int64_t batch, int64_t num_keys, int64_t num_heads,
+                  int64_t head_dim, int64_t num_queries, int64_t num_levels,
+                  int64_t num_points, int dtype, void* stream);
+
+/*
+ * Human-readable text for a return code (static storage).  The reference has
+ * no error channel below Python; this backs the RuntimeError that the host
+ * raises for a non-zero code (src/msda_triton/ops.py:165-171 raise the
+ * equivalent errors for a missing backend).
+ */
+const char* msda_error_string(int code);
+
+/* Library ABI version, (major << 16) | minor. */
+int msda_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSDA_HIP_H_ */

@@ -1,0 +1,295 @@
+// MSDA backward kernel for gfx950, plus the fill and cast kernels around it.
+//
+// Computes the reference's `_msda_backward_kernel`
+// (src/msda_triton/kernels.py:166-291).  With g = grad_out[b,q,m,:] and the
+// corner dot products G_c = <g, value[corner c]> (c = 00, 01, 10, 11):
+//   grad_attn[p]    = sum_c w_c G_c                                (254-260)
+//   grad_loc[p, x]  = A W ((1-ly)(G01 - G00) + ly (G11 - G10))     (264, 266)
+//   grad_loc[p, y]  = A H ((1-lx)(G10 - G00) + lx (G11 - G01))     (265, 267)
+//   grad_value[c]  += A w_c g            (atomic scatter, 278-291)
+// The reference forms dx/dy per channel and then reduces; because every term
+// is linear in the corner values, reducing the four corner dots first gives
+// the same sums with 4 instead of ~15 operations per channel.
+//
+// Work decomposition mirrors the forward (see msda_forward.hip): sample
+// records are staged in LDS by the whole workgroup, a pair is served by G*TS
+// lanes, G lanes span one value row.  The four G_c are folded across the G
+// chunk lanes with DPP, the per-sample results go back through LDS and leave
+// as one coalesced store per pass.  The scatter issues, per corner and lane,
+// CB-byte worth of buffer atomics: fp32 adds into an fp32 accumulator, or
+// packed fp16 / bf16 adds straight into grad_value.  Out-of-map corners carry
+// an out-of-range offset, so their atomics are dropped by the hardware.
+#include "msda_launch.h"
+
+namespace msda {
+
+namespace {
+
+constexpr int kUnroll = 2;
+
+// Scatter kVec contributions (coef * g[k]) of one corner into the accumulator.
+template <class T, class A, int CB>
+__device__ __forceinline__ void scatter(__amdgpu_buffer_rsrc_t r, uint32_t off, float coef,
+                                        const float* g) {
+  constexpr int kVec = CB / T::kBytes;
+  if constexpr (A::kBytes == 4) {
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) {
+      __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(coef * g[k], r, (int)(off + 4 * k), 0, 0);
+    }
+  } else if constexpr (kVec == 1) {
+    // A lone half element: no 16-bit atomic exists, use the packed add on the
+    // enclosing aligned word with a zero in the other lane.
+    const uint32_t word = off & ~3u;
+    const float v = coef * g[0];
+    const bool hi = (off & 2u) != 0;
+    if constexpr (A::kCode == kBF16) {
+      bf16x2 x = {(__bf16)(hi ? 0.f : v), (__bf16)(hi ? v : 0.f)};
+      raw_buffer_atomic_fadd_v2bf16(x, r, (int)word, 0, 0);
+    } else {
+      f16x2 x = {(_Float16)(hi ? 0.f : v), (_Float16)(hi ? v : 0.f)};
+      __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_v2f16(x, r, (int)word, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kVec / 2; ++k) {
+      const float lo = coef * g[2 * k], hi = coef * g[2 * k + 1];
+      if constexpr (A::kCode == kBF16) {
+        bf16x2 x = {(__bf16)lo, (__bf16)hi};
+        raw_buffer_atomic_fadd_v2bf16(x, r, (int)(off + 4 * k), 0, 0);
+      } else {
+        f16x2 x = {(_Float16)lo, (_Float16)hi};
+        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_v2f16(x, r, (int)(off + 4 * k), 0, 0);
+      }
+    }
+  }
+}
+
+// T: storage dtype.  A: accumulator dtype (F32, or T for in-place atomics).
+template <class T, class A, int CB, int G, int TS>
+__global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
+  using C = Chunk<T, CB>;
+  constexpr int kVec = C::kVec;
+  constexpr int kWords = C::kWords;
+  constexpr bool kStatic = G > 0;
+  // Accumulator byte offset = value byte offset * kAccScale.
+  constexpr uint32_t kAccScale = A::kBytes / T::kBytes;
+
+  __shared__ LevelTable lt;
+  __shared__ uint4 s_off[kMaxRecords];
+  __shared__ float4 s_geo[kMaxRecords];  // lx, ly, A, -
+  __shared__ float2 s_scl[kMaxRecords];  // A*W, A*H
+  __shared__ float4 s_res[kMaxRecords];  // grad_attn, grad_x, grad_y, -
+
+  const int g = kStatic ? G : p.g_rt;
+  const int ts = kStatic ? TS : p.ts_rt;
+  const int team = g * ts;
+  const int ppw = kWave / team;
+  const int ppb = ppw * (kBlock / kWave);
+  const int blk = xcd_remap(blockIdx.x, p.nblocks);
+  const int pair0 = blk * ppb;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int ch = lane & (g - 1);
+  const int sl = (lane / g) & (ts - 1);
+  const int pl = wave * ppw + lane / team;
+  const int pair = pair0 + pl;
+  const bool live = ch < p.g_real;
+  const uint32_t chb = live ? (uint32_t)(ch * CB) : kDeadLaneBytes;
+
+  load_levels(p, lt);
+
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value, p.value_bytes);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.grad_acc, p.acc_bytes);
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.grad_out, p.gout_bytes);
+
+  // grad_out chunk of this lane's pair (zeros for tail pairs: out of range).
+  float gv[kVec];
+  C::load(rg, (uint32_t)pair * (uint32_t)(p.D * T::kBytes) + chb, gv);
+
+  __syncthreads();
+
+  const int nrec = ppb * p.sch;
+  const int nps = p.sch / ts;
+  const int rbase = pl * p.sch + sl;
+
+  for (int pass = 0; pass < p.npass; ++pass) {
+    for (int j = threadIdx.x; j < nrec; j += kBlock) {
+      const int jp = j >> p.log2_sch;
+      const int s = pass * p.sch + (j & (p.sch - 1));
+      const int pr = pair0 + jp;
+      const Sample q = make_sample<T>(p, lt, (uint32_t)pr, (uint32_t)s,
+                                      pr < p.npairs && s < p.LK);
+      s_off[j] = make_uint4(q.off[0] * T::kBytes, q.off[1] * T::kBytes, q.off[2] * T::kBytes,
+                            q.off[3] * T::kBytes);
+      s_geo[j] = make_float4(q.lx, q.ly, q.a, 0.f);
+      s_scl[j] = make_float2(q.a * q.fw, q.a * q.fh);
+    }
+    __syncthreads();
+
+    for (int i = 0; i < nps; i += kUnroll) {
+      uint32_t raw[kUnroll][4][kWords];
+      uint4 o[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (i + u < nps) {  // wave-uniform
+          const int j = rbase + (i + u) * ts;
+          o[u] = s_off[j];
+          C::load_raw(rv, o[u].x + chb, raw[u][0]);
+          C::load_raw(rv, o[u].y + chb, raw[u][1]);
+          C::load_raw(rv, o[u].z + chb, raw[u][2]);
+          C::load_raw(rv, o[u].w + chb, raw[u][3]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (i + u < nps) {
+          const int j = rbase + (i + u) * ts;
+          float d[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            float v[kVec];
+            C::unpack(raw[u][c], v);
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < kVec; ++k) acc += gv[k] * v[k];
+            if constexpr (kStatic) {
+              d[c] = xsum_range<1, G / 2, G>(acc);
+            } else {
+              d[c] = xsum_runtime(acc, 1, g);
+            }
+          }
+          const float4 geo = s_geo[j];
+          const float lx = geo.x, ly = geo.y, a = geo.z;
+          const float mx = 1.f - lx, my = 1.f - ly;
+          const float w00 = mx * my, w01 = lx * my, w10 = mx * ly, w11 = lx * ly;
+          if (ch == 0) {
+            const float2 sc = s_scl[j];
+            const float ga = w00 * d[0] + w01 * d[1] + w10 * d[2] + w11 * d[3];
+            const float gx = sc.x * (my * (d[1] - d[0]) + ly * (d[3] - d[2]));
+            const float gy = sc.y * (mx * (d[2] - d[0]) + lx * (d[3] - d[1]));
+            s_res[j] = make_float4(ga, gx, gy, 0.f);
+          }
+          if (live) {
+            const uint32_t cb = chb * kAccScale;
+            scatter<T, A, CB>(ra, o[u].x * kAccScale + cb, a * w00, gv);
+            scatter<T, A, CB>(ra, o[u].y * kAccScale + cb, a * w01, gv);
+            scatter<T, A, CB>(ra, o[u].z * kAccScale + cb, a * w10, gv);
+            scatter<T, A, CB>(ra, o[u].w * kAccScale + cb, a * w11, gv);
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+    for (int j = threadIdx.x; j < nrec; j += kBlock) {
+      const int jp = j >> p.log2_sch;
+      const int s = pass * p.sch + (j & (p.sch - 1));
+      const int pr = pair0 + jp;
+      if (pr < p.npairs && s < p.LK) {
+        const uint64_t pi = (uint64_t)pr * (uint32_t)p.LK + (uint32_t)s;
+        const float4 r = s_res[j];
+        store1<T>(p.grad_attn, pi, r.x);
+        store1<T>(p.grad_loc, 2 * pi, r.y);
+        store1<T>(p.grad_loc, 2 * pi + 1, r.z);
+      }
+    }
+    if (pass + 1 < p.npass) __syncthreads();
+  }
+}
+
+template <class T, class A, int CB, int G, int TS>
+hipError_t launch_one(const Params& p, hipStream_t st) {
+  hipLaunchKernelGGL((bwd_kernel<T, A, CB, G, TS>), dim3(p.nblocks), dim3(kBlock), 0, st, p);
+  return hipGetLastError();
+}
+
+template <class T, class A>
+hipError_t dispatch(const Shape& s, const Params& p, hipStream_t st) {
+  if (s.cb == 16) {
+    switch (s.g * 100 + s.ts) {
+      case 204: return launch_one<T, A, 16, 2, 4>(p, st);
+      case 216: return launch_one<T, A, 16, 2, 16>(p, st);
+      case 404: return launch_one<T, A, 16, 4, 4>(p, st);
+      case 416: return launch_one<T, A, 16, 4, 16>(p, st);
+      case 804: return launch_one<T, A, 16, 8, 4>(p, st);
+      case 1604: return launch_one<T, A, 16, 16, 4>(p, st);
+      default: return launch_one<T, A, 16, 0, 0>(p, st);
+    }
+  }
+  if (s.cb == 8) return launch_one<T, A, 8, 0, 0>(p, st);
+  if (s.cb == 4) return launch_one<T, A, 4, 0, 0>(p, st);
+  if constexpr (T::kBytes == 2) {
+    if (s.cb == 2) return launch_one<T, A, 2, 0, 0>(p, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// Zero fill (a kernel rather than hipMemsetAsync so that captured graphs hold
+// only kernel nodes) and the fp32 -> dtype cast of the fp32 accumulator.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBlock) void zero_kernel(uint4* p, uint64_t n16, uint8_t* tail,
+                                                      int ntail) {
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n16; i += stride) {
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  if (blockIdx.x == 0 && (int)threadIdx.x < ntail) tail[threadIdx.x] = 0;
+}
+
+template <class T>
+__global__ __launch_bounds__(kBlock) void cast_kernel(const float* src, void* dst, uint64_t n) {
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  const uint64_t n4 = n / 4;
+  for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
+    const float4 v = reinterpret_cast<const float4*>(src)[i];
+    reinterpret_cast<uint2*>(dst)[i] = make_uint2(pack2<T>(v.x, v.y), pack2<T>(v.z, v.w));
+  }
+  if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+    const uint64_t i = n4 * 4 + threadIdx.x;
+    store1<T>(dst, i, src[i]);
+  }
+}
+
+int grid_for(uint64_t items) {
+  // Enough workgroups to cover 256 CUs several times; grid-stride beyond.
+  const uint64_t want = (items + kBlock - 1) / kBlock;
+  return (int)(want < 8192 ? (want ? want : 1) : 8192);
+}
+
+}  // namespace
+
+hipError_t launch_backward(int dtype, bool fp32_acc, const Shape& s, const Params& p,
+                           hipStream_t st) {
+  switch (dtype) {
+    case kF32: return dispatch<F32, F32>(s, p, st);
+    case kF16: return fp32_acc ? dispatch<F16, F32>(s, p, st) : dispatch<F16, F16>(s, p, st);
+    case kBF16: return fp32_acc ? dispatch<BF16, F32>(s, p, st) : dispatch<BF16, BF16>(s, p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_zero(void* ptr, uint64_t bytes, hipStream_t st) {
+  if (bytes == 0) return hipSuccess;
+  // Torch / hipMalloc buffers are 256-byte aligned; the tail covers the rest.
+  const uint64_t n16 = bytes / 16;
+  const int ntail = (int)(bytes - n16 * 16);
+  hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n16 ? n16 : 1)), dim3(kBlock), 0, st,
+                     static_cast<uint4*>(ptr), n16, static_cast<uint8_t*>(ptr) + n16 * 16, ntail);
+  return hipGetLastError();
+}
+
+hipError_t launch_cast(int dtype, const float* src, void* dst, uint64_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  const int grid = grid_for(n / 4 ? n / 4 : 1);
+  switch (dtype) {
+    case kF16: hipLaunchKernelGGL(cast_kernel<F16>, dim3(grid), dim3(kBlock), 0, st, src, dst, n); break;
+    case kBF16: hipLaunchKernelGGL(cast_kernel<BF16>, dim3(grid), dim3(kBlock), 0, st, src, dst, n); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace msda

@@ -1,0 +1,260 @@
+// C ABI of the MSDA operator: argument checks, batch slicing and launch-shape
+// selection around the kernels in msda_forward.hip / msda_backward.hip.
+// Declarations and the contract live in include/msda_hip.h.
+#include <stdlib.h>
+
+#include "../../include/msda_hip.h"
+#include "msda_launch.h"
+
+namespace msda {
+
+FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  f.mul = (uint32_t)((((1ull << l) - d) << 32) / d + 1);
+  f.shift = l;
+  f.d = d;
+  return f;
+}
+
+static int next_pow2(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+static int log2i(int x) {
+  int l = 0;
+  while ((1 << l) < x) ++l;
+  return l;
+}
+
+bool choose_shape(int row_bytes, int lk, int ts_pref, Shape* out) {
+  Shape s;
+  s.cb = row_bytes % 16 == 0 ? 16 : row_bytes % 8 == 0 ? 8 : row_bytes % 4 == 0 ? 4 : 2;
+  s.g_real = row_bytes / s.cb;
+  s.g = next_pow2(s.g_real);
+  if (s.g > kWave) return false;
+  int ts_max = kWave / s.g;
+  const int lk2 = next_pow2(lk);
+  if (ts_max > lk2) ts_max = lk2;
+  int ts = ts_pref > 0 ? next_pow2(ts_pref) : 4;
+  if (ts > ts_max) ts = ts_max;
+  s.ts = ts;
+  *out = s;
+  return true;
+}
+
+void finish_params(const Shape& s, Params* p) {
+  const int team = s.g * s.ts;
+  const int ppb = (kWave / team) * (kBlock / kWave);
+  int sch = next_pow2(p->LK);
+  if (sch > kMaxRecords / ppb) sch = kMaxRecords / ppb;
+  p->sch = sch;
+  p->log2_sch = log2i(sch);
+  p->npass = (p->LK + sch - 1) / sch;
+  p->nblocks = (p->npairs + ppb - 1) / ppb;
+  p->g_real = s.g_real;
+  p->g_rt = s.g;
+  p->ts_rt = s.ts;
+}
+
+static int env_int(const char* name) {
+  const char* v = getenv(name);
+  return v ? atoi(v) : 0;
+}
+
+// Launch-shape overrides for tuning sweeps: slots per pair (power of two).
+static int fwd_ts_pref() {
+  static const int v = env_int("MSDA_FWD_TS");
+  return v;
+}
+static int bwd_ts_pref() {
+  static const int v = env_int("MSDA_BWD_TS");
+  return v;
+}
+
+static int elem_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
+
+struct Dims {
+  int64_t B, S, M, D, Q, L, K;
+};
+
+static int check_dims(const Dims& d, int dtype) {
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return MSDA_ERR_UNSUPPORTED_DTYPE;
+  if (d.B < 0 || d.S < 0 || d.M < 0 || d.D < 0 || d.Q < 0 || d.L < 0 || d.K < 0)
+    return MSDA_ERR_INVALID_ARGUMENT;
+  if (d.L > kMaxLevels) return MSDA_ERR_UNSUPPORTED_SHAPE;
+  if (d.S >= (1ll << 31) || d.Q >= (1ll << 31) || d.M >= (1 << 16) || d.D >= (1 << 16) ||
+      d.K >= (1 << 16))
+    return MSDA_ERR_UNSUPPORTED_SHAPE;
+  return MSDA_OK;
+}
+
+// Largest batch slice whose value / output / sample counts fit the 32-bit
+// addressing of the kernels (0 if one batch element alone does not fit).
+static int64_t slice_batch(const Dims& d) {
+  const int64_t lim = (int64_t)kMaxSliceElems;
+  int64_t bs = d.B;
+  const int64_t per_val = d.S * d.M * d.D;
+  const int64_t per_out = d.Q * d.M * d.D;
+  const int64_t per_smp = d.Q * d.M * d.L * d.K;
+  if (per_val > 0 && lim / per_val < bs) bs = lim / per_val;
+  if (per_out > 0 && lim / per_out < bs) bs = lim / per_out;
+  if (per_smp > 0 && lim / per_smp < bs) bs = lim / per_smp;
+  return bs;
+}
+
+static int status(hipError_t e) { return e == hipSuccess ? MSDA_OK : MSDA_ERR_LAUNCH; }
+
+static void base_params(const Dims& d, int64_t b0, int64_t bs, int dtype, Params* p) {
+  const int e = elem_bytes(dtype);
+  p->S = (int32_t)d.S;
+  p->M = (int32_t)d.M;
+  p->D = (int32_t)d.D;
+  p->Q = (int32_t)d.Q;
+  p->L = (int32_t)d.L;
+  p->K = (int32_t)d.K;
+  p->LK = (int32_t)(d.L * d.K);
+  p->MD = (int32_t)(d.M * d.D);
+  p->npairs = (int32_t)(bs * d.Q * d.M);
+  p->value_bytes = (uint32_t)(bs * d.S * d.M * d.D * e);
+  p->gout_bytes = (uint32_t)(bs * d.Q * d.M * d.D * e);
+  p->div_qm = make_fastdiv((uint32_t)(d.Q * d.M > 0 ? d.Q * d.M : 1));
+  p->div_m = make_fastdiv((uint32_t)(d.M > 0 ? d.M : 1));
+  p->div_k = make_fastdiv((uint32_t)(d.K > 0 ? d.K : 1));
+  (void)b0;
+}
+
+static const char* at(const void* base, int64_t elems, int e) {
+  return static_cast<const char*>(base) + elems * e;
+}
+static char* at(void* base, int64_t elems, int e) { return static_cast<char*>(base) + elems * e; }
+
+}  // namespace msda
+
+using namespace msda;
+
+extern "C" int msda_forward(const void* value, const int64_t* spatial_shapes,
+                            const int64_t* level_start_index, const void* sampling_locations,
+                            const void* attention_weights, void* output, int64_t batch,
+                            int64_t num_keys, int64_t num_heads, int64_t head_dim,
+                            int64_t num_queries, int64_t num_levels, int64_t num_points,
+                            int dtype, void* stream) {
+  const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
+  int rc = check_dims(d, dtype);
+  if (rc != MSDA_OK) return rc;
+  const int64_t n_out = d.B * d.Q * d.M * d.D;
+  if (n_out == 0) return MSDA_OK;
+  const int64_t n_smp = d.B * d.Q * d.M * d.L * d.K;
+  if (!output || (d.L > 0 && (!spatial_shapes || !level_start_index)) ||
+      (n_smp > 0 && (!sampling_locations || !attention_weights)) ||
+      (d.B * d.S * d.M * d.D > 0 && !value))
+    return MSDA_ERR_INVALID_ARGUMENT;
+  const int e = elem_bytes(dtype);
+  Shape sh;
+  if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), fwd_ts_pref(), &sh))
+    return MSDA_ERR_UNSUPPORTED_SHAPE;
+  const int64_t bs = slice_batch(d);
+  if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  for (int64_t b0 = 0; b0 < d.B; b0 += bs) {
+    const int64_t nb = d.B - b0 < bs ? d.B - b0 : bs;
+    Params p = {};
+    base_params(d, b0, nb, dtype, &p);
+    p.value = value ? at(value, b0 * d.S * d.M * d.D, e) : nullptr;
+    p.shapes = spatial_shapes;
+    p.starts = level_start_index;
+    p.loc = sampling_locations ? at(sampling_locations, b0 * d.Q * d.M * d.L * d.K * 2, e)
+                               : nullptr;
+    p.attn = attention_weights ? at(attention_weights, b0 * d.Q * d.M * d.L * d.K, e) : nullptr;
+    p.out = at(output, b0 * d.Q * d.M * d.D, e);
+    finish_params(sh, &p);
+    rc = status(launch_forward(dtype, sh, p, st));
+    if (rc != MSDA_OK) return rc;
+  }
+  return MSDA_OK;
+}
+
+extern "C" int msda_backward(const void* value, const int64_t* spatial_shapes,
+                             const int64_t* level_start_index, const void* sampling_locations,
+                             const void* attention_weights, const void* grad_output,
+                             void* grad_value, float* grad_value_accum,
+                             void* grad_sampling_locations, void* grad_attention_weights,
+                             int64_t batch, int64_t num_keys, int64_t num_heads,
+                             int64_t head_dim, int64_t num_queries, int64_t num_levels,
+                             int64_t num_points, int dtype, void* stream) {
+  const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
+  int rc = check_dims(d, dtype);
+  if (rc != MSDA_OK) return rc;
+  const int e = elem_bytes(dtype);
+  const int64_t n_val = d.B * d.S * d.M * d.D;
+  const int64_t n_smp = d.B * d.Q * d.M * d.L * d.K;
+  const int64_t n_out = d.B * d.Q * d.M * d.D;
+  if ((n_val > 0 && (!value || !grad_value)) ||
+      (n_smp > 0 && (!sampling_locations || !attention_weights || !grad_sampling_locations ||
+                     !grad_attention_weights)) ||
+      (n_out > 0 && !grad_output) || (d.L > 0 && (!spatial_shapes || !level_start_index)))
+    return MSDA_ERR_INVALID_ARGUMENT;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // fp32 accumulation is only a separate path for half storage.
+  const bool fp32_acc = grad_value_accum != nullptr && dtype != kF32 && n_val > 0;
+  void* acc = fp32_acc ? static_cast<void*>(grad_value_accum) : grad_value;
+  const int acc_e = fp32_acc ? 4 : e;
+
+  rc = status(launch_zero(acc, (uint64_t)(n_val * acc_e), st));
+  if (rc != MSDA_OK) return rc;
+  if (n_smp > 0 && (n_out == 0 || d.S == 0)) {
+    // No channels or no keys: every sampled value is zero, so are the
+    // location and weight gradients.
+    rc = status(launch_zero(grad_sampling_locations, (uint64_t)(n_smp * 2 * e), st));
+    if (rc == MSDA_OK) rc = status(launch_zero(grad_attention_weights, (uint64_t)(n_smp * e), st));
+    if (rc != MSDA_OK) return rc;
+  } else if (n_smp > 0) {
+    Shape sh;
+    if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), bwd_ts_pref(), &sh))
+      return MSDA_ERR_UNSUPPORTED_SHAPE;
+    const int64_t bs = slice_batch(d);
+    if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
+    for (int64_t b0 = 0; b0 < d.B; b0 += bs) {
+      const int64_t nb = d.B - b0 < bs ? d.B - b0 : bs;
+      Params p = {};
+      base_params(d, b0, nb, dtype, &p);
+      const int64_t vo = b0 * d.S * d.M * d.D, so = b0 * d.Q * d.M * d.L * d.K;
+      p.value = at(value, vo, e);
+      p.shapes = spatial_shapes;
+      p.starts = level_start_index;
+      p.loc = at(sampling_locations, so * 2, e);
+      p.attn = at(attention_weights, so, e);
+      p.grad_out = at(grad_output, b0 * d.Q * d.M * d.D, e);
+      p.grad_acc = at(acc, vo, acc_e);
+      p.acc_bytes = (uint32_t)(nb * d.S * d.M * d.D * acc_e);
+      p.grad_loc = at(grad_sampling_locations, so * 2, e);
+      p.grad_attn = at(grad_attention_weights, so, e);
+      finish_params(sh, &p);
+      rc = status(launch_backward(dtype, fp32_acc, sh, p, st));
+      if (rc != MSDA_OK) return rc;
+    }
+  }
+  if (fp32_acc) {
+    rc = status(launch_cast(dtype, grad_value_accum, grad_value, (uint64_t)n_val, st));
+    if (rc != MSDA_OK) return rc;
+  }
+  return MSDA_OK;
+}
+
+extern "C" const char* msda_error_string(int code) {
+  switch (code) {
+    case MSDA_OK: return "success";
+    case MSDA_ERR_INVALID_ARGUMENT: return "invalid argument (negative size or NULL pointer)";
+    case MSDA_ERR_UNSUPPORTED_DTYPE: return "unsupported dtype (expected fp32, fp16 or bf16)";
+    case MSDA_ERR_UNSUPPORTED_SHAPE:
+      return "unsupported shape (more than 64 levels, head_dim row wider than one wave, or one "
+             "batch element beyond 2^28 elements)";
+    case MSDA_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown msda error code";
+  }
+}
+
+extern "C" int msda_abi_version(void) { return (1 << 16) | 0; }

@@ -1,0 +1,399 @@
+// Device-side building blocks shared by the MSDA forward and backward kernels
+// (gfx950 / CDNA4, wave64).
+//
+// Memory layouts follow the reference operator (src/msda_triton/kernels.py:
+// 67-82, 167-185): value (B,S,M,D), sampling_locations (B,Q,M,L,K,2),
+// attention_weights (B,Q,M,L,K), all C-contiguous.
+//
+// Addressing: every kernel works on a batch slice whose value tensor holds
+// fewer than 2^28 elements, so element offsets are 32-bit and value rows are
+// read with buffer loads (SGPR base + 32-bit VGPR byte offset).  A corner that
+// falls outside the feature map is given the element offset kOobElem; its byte
+// offset lies beyond the buffer's num_records, so the hardware range check
+// returns zero for the load and drops the atomic.  That is exactly
+// grid_sample's zeros padding and costs no per-element select.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace msda {
+
+constexpr int kBlock = 256;  // threads per workgroup: 4 wave64
+constexpr int kWave = 64;
+constexpr int kMaxLevels = 64;
+constexpr int kMaxRecords = 512;             // staged samples per workgroup pass
+constexpr uint32_t kOobElem = 1u << 28;      // element-offset sentinel
+constexpr uint32_t kDeadLaneBytes = 1u << 30;  // pushes padding lanes out of range
+constexpr uint32_t kMaxSliceElems = (1u << 28) - 1;
+// gfx9 buffer descriptor word 3: raw (untyped) 32-bit data format.
+constexpr int kRsrcWord3 = 0x00020000;
+
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Packed-bf16 buffer atomic; clang has no builtin for it, so bind the LLVM
+// intrinsic by name (lowers to buffer_atomic_pk_add_bf16 on gfx950).
+__device__ bf16x2 raw_buffer_atomic_fadd_v2bf16(bf16x2 v, __amdgpu_buffer_rsrc_t rsrc,
+                                                int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.atomic.fadd.v2bf16");
+
+// --------------------------------------------------------------------------
+// Division by a runtime constant: n / d == (umulhi(n, mul) + n) >> shift for
+// 0 <= n < 2^31 (Granlund & Montgomery 1994, round-up multiplier).
+// --------------------------------------------------------------------------
+struct FastDiv {
+  uint32_t mul;
+  uint32_t shift;
+  uint32_t d;
+};
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.mul) + n) >> f.shift;
+}
+
+// --------------------------------------------------------------------------
+// Storage dtypes.
+// --------------------------------------------------------------------------
+struct F32 {
+  static constexpr int kBytes = 4;
+  static constexpr int kCode = kF32;
+};
+struct F16 {
+  static constexpr int kBytes = 2;
+  static constexpr int kCode = kF16;
+};
+struct BF16 {
+  static constexpr int kBytes = 2;
+  static constexpr int kCode = kBF16;
+};
+
+// Two storage elements packed in one 32-bit word -> two floats.
+template <class T>
+__device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi);
+template <>
+__device__ __forceinline__ void unpack2<BF16>(uint32_t w, float& lo, float& hi) {
+  lo = __uint_as_float(w << 16);
+  hi = __uint_as_float(w & 0xffff0000u);
+}
+template <>
+__device__ __forceinline__ void unpack2<F16>(uint32_t w, float& lo, float& hi) {
+  f16x2 h = __builtin_bit_cast(f16x2, w);
+  lo = (float)h[0];
+  hi = (float)h[1];
+}
+
+// One storage element held in the low 16 bits.
+template <class T>
+__device__ __forceinline__ float unpack1(uint32_t w);
+template <>
+__device__ __forceinline__ float unpack1<BF16>(uint32_t w) {
+  return __uint_as_float(w << 16);
+}
+template <>
+__device__ __forceinline__ float unpack1<F16>(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)w);
+}
+template <>
+__device__ __forceinline__ float unpack1<F32>(uint32_t w) {
+  return __uint_as_float(w);
+}
+
+// Two floats -> two storage elements in one word (round to nearest even).
+template <class T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2<BF16>(float lo, float hi) {
+  bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<F16>(float lo, float hi) {
+  f16x2 v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+template <class T>
+__device__ __forceinline__ void store1(void* base, uint64_t i, float v);
+template <>
+__device__ __forceinline__ void store1<F32>(void* base, uint64_t i, float v) {
+  static_cast<float*>(base)[i] = v;
+}
+template <>
+__device__ __forceinline__ void store1<F16>(void* base, uint64_t i, float v) {
+  static_cast<_Float16*>(base)[i] = (_Float16)v;
+}
+template <>
+__device__ __forceinline__ void store1<BF16>(void* base, uint64_t i, float v) {
+  static_cast<__bf16*>(base)[i] = (__bf16)v;
+}
+
+template <class T>
+__device__ __forceinline__ float load1(const void* base, uint64_t i) {
+  if constexpr (T::kBytes == 4) {
+    return static_cast<const float*>(base)[i];
+  } else {
+    return unpack1<T>(static_cast<const uint16_t*>(base)[i]);
+  }
+}
+
+// (x, y) pair at element index 2*i.
+template <class T>
+__device__ __forceinline__ void load_xy(const void* base, uint64_t i, float& x, float& y) {
+  if constexpr (T::kBytes == 4) {
+    float2 v = static_cast<const float2*>(base)[i];
+    x = v.x;
+    y = v.y;
+  } else {
+    unpack2<T>(static_cast<const uint32_t*>(base)[i], x, y);
+  }
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
+                                           kRsrcWord3);
+}
+
+// --------------------------------------------------------------------------
+// Chunk = CB contiguous bytes of one value row, VEC = CB / elem floats.
+// --------------------------------------------------------------------------
+template <class T, int CB>
+struct Chunk {
+  static constexpr int kVec = CB / T::kBytes;
+  static constexpr int kWords = CB >= 4 ? CB / 4 : 1;
+
+  // Load CB bytes at byte offset `off` (out of range -> zeros), raw words.
+  __device__ __forceinline__ static void load_raw(__amdgpu_buffer_rsrc_t r, uint32_t off,
+                                                  uint32_t (&w)[kWords]) {
+    if constexpr (CB == 16) {
+      i32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+      w[0] = x[0]; w[1] = x[1]; w[2] = x[2]; w[3] = x[3];
+    } else if constexpr (CB == 8) {
+      i32x2 x = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+      w[0] = x[0]; w[1] = x[1];
+    } else if constexpr (CB == 4) {
+      w[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    } else {
+      static_assert(CB == 2, "chunk bytes");
+      w[0] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    }
+  }
+
+  // Raw words -> kVec floats.
+  __device__ __forceinline__ static void unpack(const uint32_t (&w)[kWords], float (&v)[kVec]) {
+    if constexpr (T::kBytes == 4) {
+#pragma unroll
+      for (int i = 0; i < kVec; ++i) v[i] = __uint_as_float(w[i]);
+    } else if constexpr (CB == 2) {
+      v[0] = unpack1<T>(w[0]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) unpack2<T>(w[i], v[2 * i], v[2 * i + 1]);
+    }
+  }
+
+  __device__ __forceinline__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t off,
+                                              float (&v)[kVec]) {
+    uint32_t w[kWords];
+    load_raw(r, off, w);
+    unpack(w, v);
+  }
+
+  // Store kVec floats as CB bytes of T at a 64-bit address.
+  __device__ __forceinline__ static void store(void* p, const float (&v)[kVec]) {
+    if constexpr (T::kBytes == 4) {
+      if constexpr (CB == 16) {
+        *static_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+      } else if constexpr (CB == 8) {
+        *static_cast<float2*>(p) = make_float2(v[0], v[1]);
+      } else {
+        *static_cast<float*>(p) = v[0];
+      }
+    } else if constexpr (CB == 2) {
+      store1<T>(p, 0, v[0]);
+    } else {
+      uint32_t w[kWords];
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) w[i] = pack2<T>(v[2 * i], v[2 * i + 1]);
+      if constexpr (CB == 16) {
+        *static_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else if constexpr (CB == 8) {
+        *static_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+      } else {
+        *static_cast<uint32_t*>(p) = w[0];
+      }
+    }
+  }
+};
+
+// --------------------------------------------------------------------------
+// Cross-lane sums.  `xsum<DIST, TEAM>` adds the value held DIST lanes away
+// inside aligned teams of TEAM lanes, so that after the steps DIST = s,
+// 2s, ..., TEAM/2 every lane of a team holds the sum over the lanes that
+// differ from it in those index bits.  DPP forms are used where the pattern
+// allows: quad_perm for 1 and 2, row_ror for 4 and 8 when a team covers whole
+// 16-lane rows (rotation then stays inside the lane group), and the gfx950
+// v_permlane16/32_swap pair exchanges for 16 and 32.  ds_swizzle (xor mode)
+// covers 4 and 8 inside smaller teams.
+// --------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+template <int DIST, int TEAM>
+__device__ __forceinline__ float xsum(float v) {
+  static_assert(DIST >= 1 && DIST < TEAM && TEAM <= kWave, "xsum shape");
+  if constexpr (DIST == 1) {
+    return v + dpp<0xB1>(v);  // quad_perm [1,0,3,2]
+  } else if constexpr (DIST == 2) {
+    return v + dpp<0x4E>(v);  // quad_perm [2,3,0,1]
+  } else if constexpr (DIST == 4 || DIST == 8) {
+    if constexpr (TEAM >= 16) {
+      return v + dpp<0x120 + DIST>(v);  // row_ror:DIST
+    } else {
+      return v + __builtin_bit_cast(
+                     float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v),
+                                                        (DIST << 10) | 0x1F));
+    }
+  } else if constexpr (DIST == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v),
+                                              __builtin_bit_cast(uint32_t, v), false, false);
+    return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+  } else {
+    static_assert(DIST == 32, "xsum distance");
+    auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                              __builtin_bit_cast(uint32_t, v), false, false);
+    return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+  }
+}
+
+// Sum over the lanes FIRST, 2*FIRST, ..., LAST (all powers of two) apart,
+// inside teams of TEAM lanes.
+template <int FIRST, int LAST, int TEAM>
+__device__ __forceinline__ float xsum_range(float v) {
+  if constexpr (FIRST > LAST) {
+    return v;
+  } else {
+    return xsum_range<FIRST * 2, LAST, TEAM>(xsum<FIRST, TEAM>(v));
+  }
+}
+
+// Runtime-distance variant (ds_bpermute) for launch shapes without a
+// specialised kernel: sums over distances first, 2*first, ... < end.
+__device__ __forceinline__ float xsum_runtime(float v, int first, int end) {
+  for (int d = first; d < end; d <<= 1) v += __shfl_xor(v, d);
+  return v;
+}
+
+// --------------------------------------------------------------------------
+// Kernel parameters (by value).  One launch covers a batch slice.
+// --------------------------------------------------------------------------
+struct Params {
+  const void* value;
+  const int64_t* shapes;
+  const int64_t* starts;
+  const void* loc;
+  const void* attn;
+  void* out;             // forward output
+  const void* grad_out;  // backward
+  void* grad_acc;        // backward atomic target (grad_value or fp32 scratch)
+  void* grad_loc;
+  void* grad_attn;
+  uint32_t value_bytes;  // num_records of the value buffer
+  uint32_t acc_bytes;    // num_records of the accumulator buffer
+  uint32_t gout_bytes;   // num_records of grad_out
+  int32_t S, M, D, Q, L, K, LK;
+  int32_t MD;
+  int32_t npairs;   // pairs (b, q, m) in the slice
+  int32_t nblocks;  // workgroups in the grid
+  int32_t sch;      // staged samples per pair per pass (power of two)
+  int32_t log2_sch;
+  int32_t npass;    // ceil(LK / sch)
+  int32_t g_real;   // live chunk lanes per value row
+  int32_t g_rt;     // runtime G (generic kernels)
+  int32_t ts_rt;    // runtime TS (generic kernels)
+  FastDiv div_qm, div_m, div_k;
+};
+
+// Workgroups are dispatched to the 8 XCDs round-robin (id i -> XCD i % 8).
+// Map them so that each XCD walks one contiguous range of logical blocks:
+// neighbouring query blocks then share that XCD's L2.  Bijective for any n.
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  constexpr int kXcd = 8;
+  const int q = n / kXcd, r = n % kXcd;
+  const int x = bid % kXcd, k = bid / kXcd;
+  return (x < r) ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
+}
+
+// Level table (H, W, start) in LDS, loaded once per workgroup.
+struct LevelTable {
+  int32_t h[kMaxLevels];
+  int32_t w[kMaxLevels];
+  int32_t start[kMaxLevels];
+};
+
+__device__ __forceinline__ void load_levels(const Params& p, LevelTable& t) {
+  for (int l = threadIdx.x; l < p.L; l += kBlock) {
+    t.h[l] = (int32_t)p.shapes[2 * l];
+    t.w[l] = (int32_t)p.shapes[2 * l + 1];
+    t.start[l] = (int32_t)p.starts[l];
+  }
+}
+
+// Bilinear geometry of one sample (pair, s), shared by both directions.
+// Coordinates follow x = loc_x * W - 0.5 (src/msda_triton/kernels.py:112-128),
+// evaluated without contraction so that it rounds like grid_sample's
+// unnormalisation.  Floors are clamped before the float->int conversion.
+struct Sample {
+  uint32_t off[4];  // element offsets of corners 00, 01, 10, 11 (kOobElem if outside)
+  float lx, ly, a, fw, fh;
+};
+
+template <class T>
+__device__ __forceinline__ Sample make_sample(const Params& p, const LevelTable& lt,
+                                              uint32_t pair, uint32_t s, bool valid) {
+  Sample r;
+  if (!valid) {
+    r.off[0] = r.off[1] = r.off[2] = r.off[3] = kOobElem;
+    r.lx = r.ly = r.a = r.fw = r.fh = 0.f;
+    return r;
+  }
+  const uint32_t b = fdiv(pair, p.div_qm);
+  const uint32_t m = pair - fdiv(pair, p.div_m) * (uint32_t)p.M;
+  const uint32_t l = fdiv(s, p.div_k);
+  const uint64_t pi = (uint64_t)pair * (uint32_t)p.LK + s;
+  float locx, locy;
+  load_xy<T>(p.loc, pi, locx, locy);
+  const float a = load1<T>(p.attn, pi);
+  const int32_t H = lt.h[l], W = lt.w[l], st = lt.start[l];
+  const float fw = (float)W, fh = (float)H;
+  const float x = __fsub_rn(__fmul_rn(locx, fw), 0.5f);
+  const float y = __fsub_rn(__fmul_rn(locy, fh), 0.5f);
+  float x0f = floorf(x), y0f = floorf(y);
+  r.lx = x - x0f;
+  r.ly = y - y0f;
+  x0f = fminf(fmaxf(x0f, -2.f), fw + 1.f);
+  y0f = fminf(fmaxf(y0f, -2.f), fh + 1.f);
+  const int32_t x0 = (int32_t)x0f, y0 = (int32_t)y0f;
+  const bool vx0 = (x0 >= 0) & (x0 < W), vx1 = (x0 >= -1) & (x0 < W - 1);
+  const bool vy0 = (y0 >= 0) & (y0 < H), vy1 = (y0 >= -1) & (y0 < H - 1);
+  const uint32_t base = (b * (uint32_t)p.S * (uint32_t)p.M + m) * (uint32_t)p.D;
+  const uint32_t o00 = base + (uint32_t)(st + y0 * W + x0) * (uint32_t)p.MD;
+  const uint32_t o10 = o00 + (uint32_t)W * (uint32_t)p.MD;
+  r.off[0] = (vy0 & vx0) ? o00 : kOobElem;
+  r.off[1] = (vy0 & vx1) ? o00 + (uint32_t)p.MD : kOobElem;
+  r.off[2] = (vy1 & vx0) ? o10 : kOobElem;
+  r.off[3] = (vy1 & vx1) ? o10 + (uint32_t)p.MD : kOobElem;
+  r.a = a;
+  r.fw = fw;
+  r.fh = fh;
+  return r;
+}
+
+}  // namespace msda

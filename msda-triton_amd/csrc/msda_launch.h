@@ -1,0 +1,36 @@
+// Host-side launch plumbing shared by the forward/backward translation units
+// and the C ABI (msda_capi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "msda_device.h"
+
+namespace msda {
+
+// Launch shape of one kernel call: CB bytes per lane load, G lanes per value
+// row (power of two, g_real of them live), TS sample slots per (b, q, m) pair.
+struct Shape {
+  int cb;
+  int g;
+  int g_real;
+  int ts;
+};
+
+FastDiv make_fastdiv(uint32_t d);
+
+// Picks CB/G for a row of `row_bytes` and the slot count TS for LK samples.
+// Returns false if the row is too wide for one wave.
+bool choose_shape(int row_bytes, int lk, int ts_pref, Shape* out);
+
+// Fills the pass/record fields of `p` for shape `s` (sch, npass, nblocks).
+void finish_params(const Shape& s, Params* p);
+
+hipError_t launch_forward(int dtype, const Shape& s, const Params& p, hipStream_t st);
+hipError_t launch_backward(int dtype, bool fp32_acc, const Shape& s, const Params& p,
+                           hipStream_t st);
+hipError_t launch_zero(void* ptr, uint64_t bytes, hipStream_t st);
+hipError_t launch_cast(int dtype, const float* src, void* dst, uint64_t n, hipStream_t st);
+
+}  // namespace msda

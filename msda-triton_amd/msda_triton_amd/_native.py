@@ -1,0 +1,72 @@
+"""ctypes binding of libmsda_hip.so, the C ABI declared in include/msda_hip.h.
+
+The library is loaded lazily, on the first call that needs it, so that the
+package imports on machines without ROCm or without a built library (the
+reference likewise imports without its GPU backend and raises at call time,
+src/msda_triton/ops.py:11-16,170-171).  There is no fallback: every device
+computation goes through this library or raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+LIB_NAME = "libmsda_hip.so"
+LIB_PATH = Path(os.environ.get("MSDA_HIP_LIB", Path(__file__).resolve().parent / LIB_NAME))
+
+DTYPE_F32 = 0
+DTYPE_F16 = 1
+DTYPE_BF16 = 2
+
+MSDA_OK = 0
+
+# Every symbol the header declares, with its ctypes signature.
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+SIGNATURES = {
+    "msda_forward": (_INT, [_P, _P, _P, _P, _P, _P] + [_I64] * 7 + [_INT, _P]),
+    "msda_backward": (_INT, [_P] * 10 + [_I64] * 7 + [_INT, _P]),
+    "msda_error_string": (ctypes.c_char_p, [_INT]),
+    "msda_abi_version": (_INT, []),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class NativeLibraryError(RuntimeError):
+    """libmsda_hip.so is missing or failed to load."""
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library with typed entry points."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise NativeLibraryError(
+                    f"the HIP path requires {LIB_PATH}, which is not built; run "
+                    "`python msda-triton_amd/build.py` (or __graft_entry__.build())"
+                )
+            try:
+                lib = ctypes.CDLL(str(LIB_PATH))
+            except OSError as exc:  # e.g. no ROCm runtime on this machine
+                raise NativeLibraryError(f"failed to load {LIB_PATH}: {exc}") from exc
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != MSDA_OK:
+        msg = load().msda_error_string(rc).decode()
+        raise RuntimeError(f"{what} failed with code {rc}: {msg}")

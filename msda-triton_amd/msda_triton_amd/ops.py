@@ -1,0 +1,190 @@
+"""Public MSDA operator on MI355X: HIP kernels (libmsda_hip.so) behind a
+torch.autograd.Function.
+
+Mirrors the reference's operator boundary, src/msda_triton/ops.py:96-199
+(validation, defaults, early return) and its autograd Function,
+src/msda_triton/ops.py:36-93, with the Triton launches replaced by calls into
+the C ABI of include/msda_hip.h.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from . import _native
+
+_FLOAT_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+_DTYPE_CODE = {
+    torch.float32: _native.DTYPE_F32,
+    torch.float16: _native.DTYPE_F16,
+    torch.bfloat16: _native.DTYPE_BF16,
+}
+
+
+def _use_fp32_grad_accum(value: torch.Tensor) -> bool:
+    """Default accumulator for grad_value (reference: src/msda_triton/ops.py:
+    21-33, which picks fp32 only where the dtype's atomic add would be an
+    emulated compare-and-swap loop).  gfx950 has native fp32, packed-fp16 and
+    packed-bf16 global atomics, so the native-dtype path is used for every
+    dtype, as the reference does on SM >= 9.0.  Pass ``fp32_grad_accum=True``
+    when many samples land on the same corners (the native half-precision sum
+    then rounds at every add)."""
+    del value
+    return False
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+class _MSDAFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, value, spatial_shapes, level_start_index, sampling_locations,
+                attention_weights, fp32_grad_accum):
+        B, S, M, D = value.shape
+        _, Q, _, L, K, _ = sampling_locations.shape
+        lib = _native.load()
+        out = value.new_empty(B, Q, M, D)
+        with torch.cuda.device(value.device):
+            rc = lib.msda_forward(
+                _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index),
+                _ptr(sampling_locations), _ptr(attention_weights), _ptr(out),
+                B, S, M, D, Q, L, K, _DTYPE_CODE[value.dtype], _stream(value),
+            )
+        _native.check(rc, "msda_forward")
+        ctx.save_for_backward(value, spatial_shapes, level_start_index,
+                              sampling_locations, attention_weights)
+        ctx.fp32_grad_accum = fp32_grad_accum
+        return out.view(B, Q, M * D)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_out):
+        value, spatial_shapes, level_start_index, sampling_locations, attention_weights = (
+            ctx.saved_tensors
+        )
+        B, S, M, D = value.shape
+        _, Q, _, L, K, _ = sampling_locations.shape
+        grad_out = grad_out.reshape(B, Q, M, D).contiguous()
+        lib = _native.load()
+
+        grad_value = torch.empty_like(value)  # zero-filled by the library
+        accum = None
+        if ctx.fp32_grad_accum and value.dtype != torch.float32:
+            accum = torch.empty(value.shape, dtype=torch.float32, device=value.device)
+        grad_loc = torch.empty_like(sampling_locations)
+        grad_attn = torch.empty_like(attention_weights)
+
+        with torch.cuda.device(value.device):
+            rc = lib.msda_backward(
+                _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index),
+                _ptr(sampling_locations), _ptr(attention_weights), _ptr(grad_out),
+                _ptr(grad_value), _ptr(accum), _ptr(grad_loc), _ptr(grad_attn),
+                B, S, M, D, Q, L, K, _DTYPE_CODE[value.dtype], _stream(value),
+            )
+        _native.check(rc, "msda_backward")
+        return grad_value, None, None, grad_loc, grad_attn, None
+
+
+def multi_scale_deformable_attention(
+    value: torch.Tensor,
+    spatial_shapes: torch.Tensor,
+    level_start_index: torch.Tensor | None,
+    sampling_locations: torch.Tensor,
+    attention_weights: torch.Tensor,
+    *,
+    fp32_grad_accum: bool | None = None,
+) -> torch.Tensor:
+    """Multi-scale deformable attention (Zhu et al. 2021, Eq. 1) on MI355X.
+
+    For each query, head, feature level l and sampling point k, bilinearly
+    samples ``value`` at ``sampling_locations`` and aggregates the samples
+    weighted by ``attention_weights``.  Sampling uses ``x_im = x * W_l - 0.5``
+    (== ``grid_sample`` with ``align_corners=False, padding_mode="zeros"``).
+    Same signature and semantics as the reference,
+    src/msda_triton/ops.py:96-138.
+
+    Args:
+        value: ``(B, S, M, D)`` flattened multi-scale feature maps,
+            ``S = sum_l H_l * W_l``, ``M`` heads, head dim ``D``.
+        spatial_shapes: ``(L, 2)`` integer ``(H_l, W_l)`` per level.
+        level_start_index: ``(L,)`` integer offset of each level along ``S``,
+            or ``None`` to compute it from ``spatial_shapes``.
+        sampling_locations: ``(B, Q, M, L, K, 2)`` normalized ``(x, y)``;
+            locations outside ``[0, 1]`` sample zeros.
+        attention_weights: ``(B, Q, M, L, K)``.
+        fp32_grad_accum: accumulate ``grad_value`` in an fp32 scratch buffer
+            (rounded once to the value dtype) instead of native-dtype atomics.
+            ``None`` selects the native atomics (see ``_use_fp32_grad_accum``).
+
+    Returns:
+        ``(B, Q, M * D)`` output, same dtype as ``value``.
+
+    Note:
+        ``grad_value`` is accumulated with atomics, so its backward is not
+        bitwise deterministic.
+    """
+    if value.dim() != 4:
+        raise ValueError(f"value must be (B, S, M, D), got {tuple(value.shape)}")
+    if sampling_locations.dim() != 6 or sampling_locations.shape[-1] != 2:
+        raise ValueError(
+            f"sampling_locations must be (B, Q, M, L, K, 2), got {tuple(sampling_locations.shape)}"
+        )
+    B, S, M, D = value.shape
+    _, Q, _, L, K, _ = sampling_locations.shape
+    if sampling_locations.shape[0] != B or sampling_locations.shape[2] != M:
+        raise ValueError(
+            f"sampling_locations {tuple(sampling_locations.shape)} inconsistent with value "
+            f"{tuple(value.shape)}"
+        )
+    if attention_weights.shape != (B, Q, M, L, K):
+        raise ValueError(
+            f"attention_weights must be {(B, Q, M, L, K)}, got {tuple(attention_weights.shape)}"
+        )
+    if spatial_shapes.shape != (L, 2):
+        raise ValueError(f"spatial_shapes must be ({L}, 2), got {tuple(spatial_shapes.shape)}")
+    if not (value.dtype == sampling_locations.dtype == attention_weights.dtype):
+        raise ValueError(
+            f"value/sampling_locations/attention_weights dtypes must match, got "
+            f"{value.dtype}/{sampling_locations.dtype}/{attention_weights.dtype}"
+        )
+    if value.dtype not in _FLOAT_DTYPES:
+        raise ValueError(f"unsupported dtype {value.dtype}; use fp32, fp16 or bf16")
+    if value.device.type != "cuda":
+        raise ValueError(
+            "the operator requires CUDA-API (ROCm/HIP) device tensors; for CPU use a "
+            "grid_sample-based reference implementation"
+        )
+    if not (value.device == sampling_locations.device == attention_weights.device):
+        raise ValueError("value, sampling_locations and attention_weights must share a device")
+
+    spatial_shapes = spatial_shapes.to(device=value.device, dtype=torch.int64).contiguous()
+    if level_start_index is None:
+        hw = spatial_shapes.prod(-1)
+        level_start_index = torch.cat([hw.new_zeros(1), hw.cumsum(0)[:-1]])
+    else:
+        if level_start_index.shape != (L,):
+            raise ValueError(
+                f"level_start_index must be ({L},), got {tuple(level_start_index.shape)}"
+            )
+        level_start_index = level_start_index.to(device=value.device, dtype=torch.int64).contiguous()
+
+    if B == 0 or Q == 0:
+        return value.new_zeros(B, Q, M * D)
+
+    if fp32_grad_accum is None:
+        fp32_grad_accum = _use_fp32_grad_accum(value)
+
+    return _MSDAFunction.apply(
+        value.contiguous(),
+        spatial_shapes,
+        level_start_index,
+        sampling_locations.contiguous(),
+        attention_weights.contiguous(),
+        bool(fp32_grad_accum),
+    )

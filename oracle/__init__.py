@@ -1,0 +1,24 @@
+"""CPU oracle for the MSDA operator -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this package, and only as the checker (or, in bench.py, as the CPU
+baseline that is timed beside the GPU).  The product path
+(msda-triton_amd/) never imports it and has no CPU fallback.
+
+Contents (msda_reference.py), each restating a function of the reference
+roulbac/msda-triton:
+  msda_reference          per-level F.grid_sample      tests/reference_impls.py:12-45
+  msda_naive              float64 loops                tests/reference_impls.py:48-87
+  msda_backward_analytic  flat-index hand gradients    labs/solutions/lab07.py:12-104
+  run_reference_fp32      fp32 CPU upcast protocol     tests/test_msda.py:80-93
+Every function is pinned by tests/test_oracle.py (naive vs grid_sample in
+float64, closed forms, gradcheck, adjoint identity, planted-mistake checks).
+"""
+
+from .msda_reference import (  # noqa: F401
+    level_start_index_of,
+    msda_backward_analytic,
+    msda_naive,
+    msda_reference,
+    run_reference_fp32,
+)

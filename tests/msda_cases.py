@@ -1,0 +1,62 @@
+"""Shared test inputs and tolerances.
+
+`make_inputs` restates the reference's seeded generator
+(tests/test_msda.py:65-77: value randn -> loc rand -> attn rand + softmax over
+L*K, CPU torch.Generator), so the same seeds give the same bits.  Tolerances
+are the reference's assert_close values (tests/test_msda.py:43-55) plus the
+norm-relative bounds of the operator's accuracy target.
+"""
+
+import torch
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+FWD_TOL = {
+    torch.float64: dict(rtol=1e-9, atol=1e-10),
+    torch.float32: dict(rtol=1e-5, atol=1e-5),
+    torch.float16: dict(rtol=5e-3, atol=5e-3),
+    torch.bfloat16: dict(rtol=3e-2, atol=3e-2),
+}
+BWD_TOL = {
+    torch.float32: dict(rtol=1e-4, atol=1e-4),
+    torch.float16: dict(rtol=3e-2, atol=3e-2),
+    torch.bfloat16: dict(rtol=8e-2, atol=8e-2),
+}
+# Norm-relative error bounds, rel_err(x, ref) = ||x - ref||_2 / ||ref||_2:
+# forward 1e-5 (fp32) / 1e-2 (fp16, bf16); each gradient 1e-4 / 2e-2.
+FWD_RELERR = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+BWD_RELERR = {torch.float32: 1e-4, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+
+CASES = [
+    dict(id="decoder", B=2, Q=100, M=4, D=32, K=4, shapes=[(24, 32), (12, 16), (6, 8)]),
+    dict(id="single_level_point", B=1, Q=17, M=1, D=16, K=1, shapes=[(13, 9)]),
+    dict(id="nonpow2_D", B=2, Q=33, M=2, D=24, K=3, shapes=[(10, 14), (5, 7)]),
+    dict(id="wide", B=1, Q=64, M=8, D=64, K=4, shapes=[(16, 16), (8, 8)]),
+]
+
+
+def case_kwargs(case):
+    return {k: v for k, v in case.items() if k != "id"}
+
+
+def make_inputs(B, Q, M, D, shapes, K, dtype, device, loc_lo=0.0, loc_hi=1.0, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    L = len(shapes)
+    S = sum(h * w for h, w in shapes)
+    value = torch.randn(B, S, M, D, generator=gen).to(device, dtype)
+    loc = loc_lo + (loc_hi - loc_lo) * torch.rand(B, Q, M, L, K, 2, generator=gen)
+    loc = loc.to(device, dtype)
+    attn = torch.rand(B, Q, M, L, K, generator=gen)
+    attn = attn.flatten(3).softmax(-1).view(B, Q, M, L, K).to(device, dtype)
+    spatial_shapes = torch.tensor(shapes, dtype=torch.long, device=device)
+    hw = spatial_shapes.prod(-1)
+    starts = torch.cat([hw.new_zeros(1), hw.cumsum(0)[:-1]])
+    return value, spatial_shapes, starts, loc, attn
+
+
+def rel_err(x: torch.Tensor, ref: torch.Tensor) -> float:
+    x = x.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    den = ref.norm().item()
+    num = (x - ref).norm().item()
+    return num / den if den > 0 else num
