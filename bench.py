@@ -1,0 +1,294 @@
+#!/usr/bin/env python3
+"""MSDA benchmark on one MI355X: the reference's headline workload.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--preset decoder]
+
+One step = one forward + one backward (all three gradients, grad_value
+zero-fill included) of multi-scale deformable attention over one batch of the
+preset's synthetic inputs, already resident in HBM.  Steps are launched
+through the C ABI (libmsda_hip.so) and replayed from a HIP graph, so the
+timed region measures the device, not the Python launcher (the reference's
+published numbers are device times too: benchmarks/modal_benchmark.py:101-124).
+
+Prints ONE JSON line:
+  value        algorithmic GB/s of the fwd+bwd step (bytes by the reference's
+               accounting, labs/03_the_machine.py:232-251)
+  ms_per_step  fwd+bwd wall time per step over the K timed steps
+  fwd_us / bwd_us / fwd_gbps ...  per-call device times from HIP events around
+               graph replays of R calls (bwd = zero-fill + backward kernel)
+  roofline     backward pass (the dominant cost) vs 8 TB/s HBM
+  roofline_fwd forward kernel vs 8 TB/s HBM (the operator's stated target)
+  cpu_baseline the CPU oracle (grid_sample restatement) on the host cores
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "msda-triton_amd"))
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def _traffic(preset: str, kernel: str):
+    """HBM bytes per launch measured offline with rocprofv3 --pmc
+    (FETCH_SIZE + WRITE_SIZE, scaled by a copy-kernel calibration), recorded
+    in profiles/traffic_<preset>.txt as `<kernel>: <bytes>` lines."""
+    path = ROOT / "profiles" / f"traffic_{preset}.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith(kernel + ":"):
+            try:
+                return int(float(line.split(":", 1)[1].split()[0]))
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline(preset: str, max_seconds: float = 25.0) -> dict:
+    """The oracle (msda_reference restatement: per-level F.grid_sample + torch
+    autograd) on fp32 upcasts of the same inputs, fwd+bwd, on this host's
+    cores: 1 warm-up, then the median of up to 5 runs within ~max_seconds."""
+    import torch
+
+    from msda_triton_amd import presets
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import run_reference_fp32
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    value, shapes, _, loc, attn = presets.make_preset_inputs(preset, device="cpu")
+    g = presets.make_grad_out(preset, device="cpu")
+    run_reference_fp32(value, shapes, loc, attn, g)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start) < max_seconds:
+        t0 = time.perf_counter()
+        run_reference_fp32(value, shapes, loc, attn, g)
+        times.append(time.perf_counter() - t0)
+    fwd_b, bwd_b = presets.algorithmic_bytes(preset)
+    t = statistics.median(times)
+    return {
+        "value": round((fwd_b + bwd_b) / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{preset} preset, full batch, fwd+bwd of the grid_sample oracle in fp32 "
+                  f"(median of {len(times)} runs, {t * 1e3:.1f} ms each) on {_cpu_model()}",
+        "ms_per_step": round(t * 1e3, 3),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description="MSDA fwd+bwd benchmark (one MI355X)")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--preset", default="decoder")
+    ap.add_argument("--fp32-grad-accum", action="store_true",
+                    help="accumulate grad_value in an fp32 scratch buffer")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the MSDA operator has no multi-GPU path in this "
+              "build (batch/head sharding needs no communication; see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from msda_triton_amd import _native, presets
+    from msda_triton_amd.ops import _DTYPE_CODE
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    lib = _native.load()
+
+    c = presets.preset_dims(args.preset)
+    B, S, M, D, Q, L, K = c["B"], c["S"], c["M"], c["D"], c["Q"], c["L"], c["K"]
+    value, shapes, starts, loc, attn = presets.make_preset_inputs(args.preset, device=dev)
+    grad_out = presets.make_grad_out(args.preset, device=dev)
+    out = torch.empty(B, Q, M, D, dtype=value.dtype, device=dev)
+    grad_value = torch.empty_like(value)
+    grad_loc = torch.empty_like(loc)
+    grad_attn = torch.empty_like(attn)
+    accum = (torch.empty(value.shape, dtype=torch.float32, device=dev)
+             if args.fp32_grad_accum and value.dtype != torch.float32 else None)
+    dt = _DTYPE_CODE[value.dtype]
+    dims = (B, S, M, D, Q, L, K)
+
+    def fwd():
+        st = torch.cuda.current_stream().cuda_stream
+        rc = lib.msda_forward(value.data_ptr(), shapes.data_ptr(), starts.data_ptr(),
+                              loc.data_ptr(), attn.data_ptr(), out.data_ptr(), *dims, dt, st)
+        _native.check(rc, "msda_forward")
+
+    def bwd():
+        st = torch.cuda.current_stream().cuda_stream
+        rc = lib.msda_backward(value.data_ptr(), shapes.data_ptr(), starts.data_ptr(),
+                               loc.data_ptr(), attn.data_ptr(), grad_out.data_ptr(),
+                               grad_value.data_ptr(), None if accum is None else accum.data_ptr(),
+                               grad_loc.data_ptr(), grad_attn.data_ptr(), *dims, dt, st)
+        _native.check(rc, "msda_backward")
+
+    def step():
+        fwd()
+        bwd()
+
+    def capture(fn, reps):
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        torch.cuda.synchronize()
+        return graph
+
+    step_graph = capture(step, 1)
+    for _ in range(args.warmup):
+        step_graph.replay()
+    torch.cuda.synchronize()
+
+    # Timed region: exactly K steps, synchronised on both sides.
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step_graph.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / args.steps * 1e3
+
+    # Per-call device times: HIP events on the launch stream around replays of
+    # graphs holding R back-to-back calls.
+    def per_call_us(fn, reps=50, replays=10):
+        graph = capture(fn, reps)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * replays)
+
+    fwd_us = per_call_us(fwd)
+    bwd_us = per_call_us(bwd)
+    step_us = per_call_us(step, reps=25)
+
+    # Through the public autograd operator, eagerly (host launch cost included).
+    from msda_triton_amd import multi_scale_deformable_attention as msda
+
+    v_l = value.clone().requires_grad_(True)
+    l_l = loc.clone().requires_grad_(True)
+    a_l = attn.clone().requires_grad_(True)
+    g_flat = grad_out.view(B, Q, M * D)
+
+    def api_step():
+        o = msda(v_l, shapes, starts, l_l, a_l, fp32_grad_accum=args.fp32_grad_accum)
+        o.backward(g_flat)
+
+    for _ in range(5):
+        api_step()
+    torch.cuda.synchronize()
+    n_api = 50
+    t0 = time.perf_counter()
+    for _ in range(n_api):
+        api_step()
+    torch.cuda.synchronize()
+    api_us = (time.perf_counter() - t0) / n_api * 1e6
+
+    fwd_b, bwd_b = presets.algorithmic_bytes(args.preset)
+    value_gbps = (fwd_b + bwd_b) / (ms_per_step * 1e-3) / 1e9
+    bwd_gbps = bwd_b / (bwd_us * 1e-6) / 1e9
+    fwd_gbps = fwd_b / (fwd_us * 1e-6) / 1e9
+    dtype_name = {torch.float32: "fp32", torch.float16: "fp16", torch.bfloat16: "bf16"}[value.dtype]
+
+    record = {
+        "metric": "MSDA fwd+bwd algorithmic HBM GB/s (with fwd and fwd+bwd ms), "
+                  f"{args.preset} preset B{B} Q{Q} {dtype_name} (1 GPU)",
+        "value": round(value_gbps, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32-accumulate/" + dtype_name,
+        "data": "synthetic (seeded CPU generator, preset distributions)",
+        "config": {
+            "workload": f"msda_{args.preset}_fwd_bwd",
+            "B": B, "Q": Q, "M": M, "D": D, "L": L, "K": K, "S": S,
+            "spatial_shapes": c["shapes"],
+            "grad_value_accum": "fp32" if accum is not None else dtype_name,
+            "timing": "HIP-graph replay of C-ABI calls; inputs resident in HBM",
+        },
+        "fwd_us": round(fwd_us, 3),
+        "bwd_us": round(bwd_us, 3),
+        "fwd_bwd_us": round(step_us, 3),
+        "fwd_gbps": round(fwd_gbps, 1),
+        "bwd_gbps": round(bwd_gbps, 1),
+        "api_eager_fwd_bwd_us": round(api_us, 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(bwd_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(bwd_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": _traffic(args.preset, "backward"),
+            "kernel": "msda_backward call (zero-fill + bwd_kernel)",
+            "algorithmic_bytes": bwd_b,
+        },
+        "roofline_fwd": {
+            "bound": "hbm",
+            "achieved": round(fwd_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(fwd_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": _traffic(args.preset, "forward"),
+            "kernel": "fwd_kernel",
+            "algorithmic_bytes": fwd_b,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        record["cpu_baseline"] = cpu_baseline(args.preset)
+    print(json.dumps(record), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -15,55 +15,93 @@
 // records are staged in LDS by the whole workgroup, a pair is served by G*TS
 // lanes, G lanes span one value row.  The four G_c are folded across the G
 // chunk lanes with DPP, the per-sample results go back through LDS and leave
-// as one coalesced store per pass.  The scatter issues, per corner and lane,
-// CB-byte worth of buffer atomics: fp32 adds into an fp32 accumulator, or
-// packed fp16 / bf16 adds straight into grad_value.  Out-of-map corners carry
-// an out-of-range offset, so their atomics are dropped by the hardware.
+// as one coalesced store per pass.  The scatter (see Scatter below) issues
+// buffer atomics whose lanes cover consecutive words of each corner row: fp32
+// adds into an fp32 accumulator, or packed fp16 / bf16 adds straight into
+// grad_value.  Out-of-map corners carry an out-of-range offset, so their
+// atomics are dropped by the hardware.  The backward prefers 16 lanes per
+// value row (4-byte gathers for a 64-byte bf16 row) and one sample slot per
+// pair, so that one atomic instruction covers four full rows of four
+// different (b, q, m) pairs.
 #include "msda_launch.h"
 
 namespace msda {
 
 namespace {
 
-constexpr int kUnroll = 2;
+constexpr int kUnroll = 4;
 
-// Scatter kVec contributions (coef * g[k]) of one corner into the accumulator.
+// Scatter of one corner row.  The accumulator row holds D elements of A;
+// seen as 4-byte words (one fp32 element, or a packed pair of fp16 / bf16
+// elements), live chunk lane c of the g_real lanes owns the words
+// c, c + g_real, c + 2 g_real, ...  One atomic instruction then covers
+// g_real consecutive words of every row it touches: the hardware executes
+// buffer atomics per 64-byte segment, so a full segment per instruction is
+// four times faster than the 16-byte pieces a lane's own gather chunk would
+// give.  `sg` holds this lane's grad_out values in that word order.
 template <class T, class A, int CB>
-__device__ __forceinline__ void scatter(__amdgpu_buffer_rsrc_t r, uint32_t off, float coef,
-                                        const float* g) {
-  constexpr int kVec = CB / T::kBytes;
-  if constexpr (A::kBytes == 4) {
-#pragma unroll
-    for (int k = 0; k < kVec; ++k) {
-      __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(coef * g[k], r, (int)(off + 4 * k), 0, 0);
-    }
-  } else if constexpr (kVec == 1) {
-    // A lone half element: no 16-bit atomic exists, use the packed add on the
-    // enclosing aligned word with a zero in the other lane.
-    const uint32_t word = off & ~3u;
-    const float v = coef * g[0];
-    const bool hi = (off & 2u) != 0;
-    if constexpr (A::kCode == kBF16) {
-      bf16x2 x = {(__bf16)(hi ? 0.f : v), (__bf16)(hi ? v : 0.f)};
-      raw_buffer_atomic_fadd_v2bf16(x, r, (int)word, 0, 0);
+struct Scatter {
+  static constexpr int kVec = CB / T::kBytes;
+  static constexpr int kWordsPerLane = kVec * A::kBytes / 4;  // 0: odd-D half rows
+  static constexpr int kElemsPerWord = 4 / A::kBytes;
+  static constexpr int kSlots = kWordsPerLane > 0 ? kWordsPerLane * kElemsPerWord : 1;
+
+  // grad_out values of the words this lane scatters.
+  __device__ __forceinline__ static void load_g(const Params& p, int pair, int ch, bool live,
+                                                float (&sg)[kSlots]) {
+    for (int i = 0; i < kSlots; ++i) sg[i] = 0.f;
+    if (!live || pair >= p.npairs) return;
+    const uint64_t base = (uint64_t)pair * (uint32_t)p.D;
+    if constexpr (kWordsPerLane == 0) {
+      sg[0] = load1<T>(p.grad_out, base + ch);  // CB == 2: one element per lane
     } else {
-      f16x2 x = {(_Float16)(hi ? 0.f : v), (_Float16)(hi ? v : 0.f)};
-      __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_v2f16(x, r, (int)word, 0, 0);
-    }
-  } else {
 #pragma unroll
-    for (int k = 0; k < kVec / 2; ++k) {
-      const float lo = coef * g[2 * k], hi = coef * g[2 * k + 1];
-      if constexpr (A::kCode == kBF16) {
-        bf16x2 x = {(__bf16)lo, (__bf16)hi};
-        raw_buffer_atomic_fadd_v2bf16(x, r, (int)(off + 4 * k), 0, 0);
-      } else {
-        f16x2 x = {(_Float16)lo, (_Float16)hi};
-        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_v2f16(x, r, (int)(off + 4 * k), 0, 0);
+      for (int i = 0; i < kWordsPerLane; ++i) {
+        const uint64_t e0 = base + (uint64_t)(ch + p.g_real * i) * kElemsPerWord;
+        if constexpr (kElemsPerWord == 2) {
+          load_xy<T>(p.grad_out, e0 / 2, sg[2 * i], sg[2 * i + 1]);
+        } else {
+          sg[i] = load1<T>(p.grad_out, e0);
+        }
       }
     }
   }
-}
+
+  // Add coef * sg into the row whose accumulator byte offset is `row`
+  // (out-of-range rows are dropped by the buffer range check).
+  __device__ __forceinline__ static void add(__amdgpu_buffer_rsrc_t r, uint32_t row, int ch,
+                                             int g_real, float coef, const float (&sg)[kSlots]) {
+    if constexpr (kWordsPerLane == 0) {
+      // Half storage with odd D: rows are not word aligned; add this lane's
+      // element with the packed atomic on its enclosing word, zero in the
+      // other half.
+      const uint32_t off = row + (uint32_t)ch * A::kBytes;
+      const float v = coef * sg[0];
+      const bool hi = (off & 2u) != 0;
+      if constexpr (A::kCode == kBF16) {
+        bf16x2 x = {(__bf16)(hi ? 0.f : v), (__bf16)(hi ? v : 0.f)};
+        raw_buffer_atomic_fadd_v2bf16(x, r, (int)(off & ~3u), 0, 0);
+      } else {
+        f16x2 x = {(_Float16)(hi ? 0.f : v), (_Float16)(hi ? v : 0.f)};
+        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_v2f16(x, r, (int)(off & ~3u), 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kWordsPerLane; ++i) {
+        const int off = (int)(row + 4u * (uint32_t)(ch + g_real * i));
+        if constexpr (A::kBytes == 4) {
+          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(coef * sg[i], r, off, 0, 0);
+        } else if constexpr (A::kCode == kBF16) {
+          bf16x2 x = {(__bf16)(coef * sg[2 * i]), (__bf16)(coef * sg[2 * i + 1])};
+          raw_buffer_atomic_fadd_v2bf16(x, r, off, 0, 0);
+        } else {
+          f16x2 x = {(_Float16)(coef * sg[2 * i]), (_Float16)(coef * sg[2 * i + 1])};
+          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_v2f16(x, r, off, 0, 0);
+        }
+      }
+    }
+  }
+};
 
 // T: storage dtype.  A: accumulator dtype (F32, or T for in-place atomics).
 template <class T, class A, int CB, int G, int TS>
@@ -104,9 +142,13 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.grad_acc, p.acc_bytes);
   const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.grad_out, p.gout_bytes);
 
-  // grad_out chunk of this lane's pair (zeros for tail pairs: out of range).
+  // grad_out of this lane's pair: its gather chunk (for the dot products)
+  // and the words it scatters (zeros for tail pairs and padding lanes).
   float gv[kVec];
   C::load(rg, (uint32_t)pair * (uint32_t)(p.D * T::kBytes) + chb, gv);
+  using Sc = Scatter<T, A, CB>;
+  float sg[Sc::kSlots];
+  Sc::load_g(p, pair, ch, live, sg);
 
   __syncthreads();
 
@@ -172,11 +214,10 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
             s_res[j] = make_float4(ga, gx, gy, 0.f);
           }
           if (live) {
-            const uint32_t cb = chb * kAccScale;
-            scatter<T, A, CB>(ra, o[u].x * kAccScale + cb, a * w00, gv);
-            scatter<T, A, CB>(ra, o[u].y * kAccScale + cb, a * w01, gv);
-            scatter<T, A, CB>(ra, o[u].z * kAccScale + cb, a * w10, gv);
-            scatter<T, A, CB>(ra, o[u].w * kAccScale + cb, a * w11, gv);
+            Sc::add(ra, o[u].x * kAccScale, ch, p.g_real, a * w00, sg);
+            Sc::add(ra, o[u].y * kAccScale, ch, p.g_real, a * w01, sg);
+            Sc::add(ra, o[u].z * kAccScale, ch, p.g_real, a * w10, sg);
+            Sc::add(ra, o[u].w * kAccScale, ch, p.g_real, a * w11, sg);
           }
         }
       }
@@ -207,17 +248,16 @@ hipError_t launch_one(const Params& p, hipStream_t st) {
 
 template <class T, class A>
 hipError_t dispatch(const Shape& s, const Params& p, hipStream_t st) {
-  if (s.cb == 16) {
-    switch (s.g * 100 + s.ts) {
-      case 204: return launch_one<T, A, 16, 2, 4>(p, st);
-      case 216: return launch_one<T, A, 16, 2, 16>(p, st);
-      case 404: return launch_one<T, A, 16, 4, 4>(p, st);
-      case 416: return launch_one<T, A, 16, 4, 16>(p, st);
-      case 804: return launch_one<T, A, 16, 8, 4>(p, st);
-      case 1604: return launch_one<T, A, 16, 16, 4>(p, st);
-      default: return launch_one<T, A, 16, 0, 0>(p, st);
-    }
+  switch (s.cb * 10000 + s.g * 100 + s.ts) {
+    case 40801: return launch_one<T, A, 4, 8, 1>(p, st);
+    case 41601: return launch_one<T, A, 4, 16, 1>(p, st);
+    case 41604: return launch_one<T, A, 4, 16, 4>(p, st);
+    case 81601: return launch_one<T, A, 8, 16, 1>(p, st);
+    case 161601: return launch_one<T, A, 16, 16, 1>(p, st);
+    case 160404: return launch_one<T, A, 16, 4, 4>(p, st);
+    default: break;
   }
+  if (s.cb == 16) return launch_one<T, A, 16, 0, 0>(p, st);
   if (s.cb == 8) return launch_one<T, A, 8, 0, 0>(p, st);
   if (s.cb == 4) return launch_one<T, A, 4, 0, 0>(p, st);
   if constexpr (T::kBytes == 2) {

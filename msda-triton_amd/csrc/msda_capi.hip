@@ -30,16 +30,34 @@ static int log2i(int x) {
   return l;
 }
 
-bool choose_shape(int row_bytes, int lk, int ts_pref, Shape* out) {
+bool choose_shape(int row_bytes, int lk, int64_t npairs, bool backward, int ts_pref,
+                  int cb_pref, Shape* out) {
   Shape s;
+  // Widest lane chunk (<= 16 bytes) that divides the row.
   s.cb = row_bytes % 16 == 0 ? 16 : row_bytes % 8 == 0 ? 8 : row_bytes % 4 == 0 ? 4 : 2;
+  // The backward wants >= 16 lanes per row (4-byte chunks at least) so that
+  // its atomics cover whole 64-byte segments per instruction.
+  if (backward)
+    while (s.cb > 4 && row_bytes / s.cb < 16) s.cb >>= 1;
+  while (cb_pref > 0 && s.cb > cb_pref && s.cb > 2) s.cb >>= 1;
   s.g_real = row_bytes / s.cb;
   s.g = next_pow2(s.g_real);
   if (s.g > kWave) return false;
   int ts_max = kWave / s.g;
   const int lk2 = next_pow2(lk);
   if (ts_max > lk2) ts_max = lk2;
-  int ts = ts_pref > 0 ? next_pow2(ts_pref) : 4;
+  int ts;
+  if (ts_pref > 0) {
+    ts = next_pow2(ts_pref);
+  } else if (backward) {
+    // One slot: an atomic instruction then spans different (b, q, m) pairs,
+    // whose rows differ, instead of neighbouring points of one query.
+    ts = 1;
+  } else {
+    // Split a pair's samples over 4 slots unless one slot per pair already
+    // yields >= 8192 waves (32 per CU).
+    ts = npairs * s.g / kWave >= 8192 ? 1 : 4;
+  }
   if (ts > ts_max) ts = ts_max;
   s.ts = ts;
   *out = s;
@@ -72,6 +90,15 @@ static int fwd_ts_pref() {
 }
 static int bwd_ts_pref() {
   static const int v = env_int("MSDA_BWD_TS");
+  return v;
+}
+// Upper bound on the bytes per lane load (16, 8, 4, 2).
+static int fwd_cb_pref() {
+  static const int v = env_int("MSDA_FWD_CB");
+  return v;
+}
+static int bwd_cb_pref() {
+  static const int v = env_int("MSDA_BWD_CB");
   return v;
 }
 
@@ -154,7 +181,8 @@ extern "C" int msda_forward(const void* value, const int64_t* spatial_shapes,
     return MSDA_ERR_INVALID_ARGUMENT;
   const int e = elem_bytes(dtype);
   Shape sh;
-  if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), fwd_ts_pref(), &sh))
+  if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, false, fwd_ts_pref(),
+                    fwd_cb_pref(), &sh))
     return MSDA_ERR_UNSUPPORTED_SHAPE;
   const int64_t bs = slice_batch(d);
   if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
@@ -213,7 +241,8 @@ extern "C" int msda_backward(const void* value, const int64_t* spatial_shapes,
     if (rc != MSDA_OK) return rc;
   } else if (n_smp > 0) {
     Shape sh;
-    if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), bwd_ts_pref(), &sh))
+    if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, true, bwd_ts_pref(),
+                      bwd_cb_pref(), &sh))
       return MSDA_ERR_UNSUPPORTED_SHAPE;
     const int64_t bs = slice_batch(d);
     if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;

@@ -136,17 +136,20 @@ hipError_t launch_one(const Params& p, hipStream_t st) {
 
 template <class T>
 hipError_t dispatch(const Shape& s, const Params& p, hipStream_t st) {
-  if (s.cb == 16) {
-    switch (s.g * 100 + s.ts) {
-      case 204: return launch_one<T, 16, 2, 4>(p, st);
-      case 216: return launch_one<T, 16, 2, 16>(p, st);
-      case 404: return launch_one<T, 16, 4, 4>(p, st);
-      case 416: return launch_one<T, 16, 4, 16>(p, st);
-      case 804: return launch_one<T, 16, 8, 4>(p, st);
-      case 1604: return launch_one<T, 16, 16, 4>(p, st);
-      default: return launch_one<T, 16, 0, 0>(p, st);
-    }
+  switch (s.cb * 10000 + s.g * 100 + s.ts) {
+    case 160201: return launch_one<T, 16, 2, 1>(p, st);
+    case 160204: return launch_one<T, 16, 2, 4>(p, st);
+    case 160216: return launch_one<T, 16, 2, 16>(p, st);
+    case 160401: return launch_one<T, 16, 4, 1>(p, st);
+    case 160404: return launch_one<T, 16, 4, 4>(p, st);
+    case 160416: return launch_one<T, 16, 4, 16>(p, st);
+    case 160801: return launch_one<T, 16, 8, 1>(p, st);
+    case 160804: return launch_one<T, 16, 8, 4>(p, st);
+    case 161601: return launch_one<T, 16, 16, 1>(p, st);
+    case 161604: return launch_one<T, 16, 16, 4>(p, st);
+    default: break;
   }
+  if (s.cb == 16) return launch_one<T, 16, 0, 0>(p, st);
   if (s.cb == 8) return launch_one<T, 8, 0, 0>(p, st);
   if (s.cb == 4) return launch_one<T, 4, 0, 0>(p, st);
   if constexpr (T::kBytes == 2) {

@@ -20,9 +20,11 @@ struct Shape {
 
 FastDiv make_fastdiv(uint32_t d);
 
-// Picks CB/G for a row of `row_bytes` and the slot count TS for LK samples.
+// Picks CB/G for a row of `row_bytes` and the slot count TS for LK samples
+// over `npairs` (b, q, m) pairs; *_pref > 0 override the choice (sweeps).
 // Returns false if the row is too wide for one wave.
-bool choose_shape(int row_bytes, int lk, int ts_pref, Shape* out);
+bool choose_shape(int row_bytes, int lk, int64_t npairs, bool backward, int ts_pref,
+                  int cb_pref, Shape* out);
 
 // Fills the pass/record fields of `p` for shape `s` (sch, npass, nblocks).
 void finish_params(const Shape& s, Params* p);
