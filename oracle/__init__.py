@@ -10,7 +10,7 @@ roulbac/msda-triton:
   msda_reference          per-level F.grid_sample      tests/reference_impls.py:12-45
   msda_naive              float64 loops                tests/reference_impls.py:48-87
   msda_backward_analytic  flat-index hand gradients    labs/solutions/lab07.py:12-104
-  run_reference_fp32      fp32 CPU upcast protocol     tests/test_msda.py:80-93
+  run_reference(_fp32)    CPU upcast protocol          tests/test_msda.py:80-93
 Every function is pinned by tests/test_oracle.py (naive vs grid_sample in
 float64, closed forms, gradcheck, adjoint identity, planted-mistake checks).
 """
@@ -20,5 +20,6 @@ from .msda_reference import (  # noqa: F401
     msda_backward_analytic,
     msda_naive,
     msda_reference,
+    run_reference,
     run_reference_fp32,
 )

@@ -168,17 +168,30 @@ def msda_backward_analytic(
     return grad_value.view(B, S, M, D), grad_loc, grad_attn
 
 
-def run_reference_fp32(value, spatial_shapes, loc, attn, grad_out=None):
-    """Oracle forward (and backward when grad_out is given) on fp32 CPU leaf
-    copies of the given (already dtype-rounded) inputs, as the reference's
-    tests do (tests/test_msda.py:80-93).  Returns (out, grads or None) on CPU."""
+def run_reference(value, spatial_shapes, loc, attn, grad_out=None, dtype=torch.float32):
+    """Oracle forward (and backward when grad_out is given) on CPU leaf copies
+    of the given (already dtype-rounded) inputs, upcast to `dtype`.  With
+    dtype=float32 this is the reference's test protocol (tests/test_msda.py:
+    80-93).  Returns (out, grads or None) on CPU in `dtype`.
+
+    float64 is the exact-arithmetic variant: grid_sample works on the grid
+    2*loc - 1, and in float32 that rounding moves the image coordinate by up
+    to W * 2^-25 pixels, which at W = 128 already shifts grad_loc by ~3e-4
+    and can flip the bilinear cell at a knot.  Large fp32 inputs are checked
+    against float64."""
     shapes = spatial_shapes.cpu()
-    v = value.detach().float().cpu().requires_grad_(grad_out is not None)
-    lo = loc.detach().float().cpu().requires_grad_(grad_out is not None)
-    a = attn.detach().float().cpu().requires_grad_(grad_out is not None)
-    if grad_out is None:
+    grad = grad_out is not None
+    v = value.detach().to(dtype).cpu().requires_grad_(grad)
+    lo = loc.detach().to(dtype).cpu().requires_grad_(grad)
+    a = attn.detach().to(dtype).cpu().requires_grad_(grad)
+    if not grad:
         with torch.no_grad():
             return msda_reference(v, shapes, lo, a), None
     out = msda_reference(v, shapes, lo, a)
-    out.backward(grad_out.detach().float().cpu())
+    out.backward(grad_out.detach().to(dtype).cpu())
     return out.detach(), (v.grad, lo.grad, a.grad)
+
+
+def run_reference_fp32(value, spatial_shapes, loc, attn, grad_out=None):
+    """The reference's fp32 CPU protocol (tests/test_msda.py:80-93)."""
+    return run_reference(value, spatial_shapes, loc, attn, grad_out, dtype=torch.float32)

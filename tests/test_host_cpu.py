@@ -1,0 +1,182 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports
+every symbol of include/msda_hip.h, rejects bad arguments before touching
+the device, the Python boundary validates like the reference
+(src/msda_triton/ops.py:140-184, tests/test_msda.py:253-269), and the
+benchmark presets carry the published sizes and byte counts."""
+
+import ctypes
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+from msda_cases import make_inputs
+from msda_triton_amd import _native, multi_scale_deformable_attention, presets
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "msda_hip.h"
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(msda_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _native.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = header_functions()
+    assert names == sorted(_native.SIGNATURES), names
+    for name in names:
+        assert hasattr(lib, name), name
+    syms = subprocess.run(["nm", "-D", "--defined-only", str(_native.LIB_PATH)],
+                          capture_output=True, text=True, check=True).stdout
+    for name in names:
+        assert re.search(rf"\bT {name}$", syms, re.M), name
+
+
+def test_abi_version_and_error_strings(lib):
+    assert lib.msda_abi_version() == (1 << 16)
+    for code in range(5):
+        assert lib.msda_error_string(code)
+    assert b"unknown" in lib.msda_error_string(99)
+
+
+FWD_ARGS = dict(value=1, shapes=1, starts=1, loc=1, attn=1, out=1,
+                B=2, S=10, M=2, D=8, Q=3, L=1, K=2, dtype=0)
+
+
+def call_fwd(lib, **kw):
+    a = dict(FWD_ARGS, **kw)
+    return lib.msda_forward(a["value"], a["shapes"], a["starts"], a["loc"], a["attn"], a["out"],
+                            a["B"], a["S"], a["M"], a["D"], a["Q"], a["L"], a["K"], a["dtype"], None)
+
+
+def call_bwd(lib, **kw):
+    a = dict(FWD_ARGS, gout=1, gv=1, acc=None, gl=1, ga=1)
+    a.update(kw)
+    return lib.msda_backward(a["value"], a["shapes"], a["starts"], a["loc"], a["attn"], a["gout"],
+                             a["gv"], a["acc"], a["gl"], a["ga"], a["B"], a["S"], a["M"], a["D"],
+                             a["Q"], a["L"], a["K"], a["dtype"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=7), 2),
+    (dict(B=-1), 1),
+    (dict(K=-3), 1),
+    (dict(L=65), 3),
+    (dict(D=1000), 3),            # fp32 row of 4000 bytes: wider than one wave
+    (dict(out=None), 1),
+    (dict(loc=None), 1),
+    (dict(shapes=None), 1),
+    (dict(B=0), 0),               # empty: nothing to launch
+    (dict(Q=0), 0),
+])
+def test_forward_argument_errors_return_before_any_launch(lib, kw, code):
+    assert call_fwd(lib, **kw) == code
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=3), 2),
+    (dict(gl=None), 1),
+    (dict(gout=None), 1),
+    (dict(gv=None), 1),
+    (dict(L=100), 3),
+    (dict(B=0, S=0, Q=0), 0),     # nothing to zero, nothing to launch
+])
+def test_backward_argument_errors_return_before_any_launch(lib, kw, code):
+    assert call_bwd(lib, **kw) == code
+
+
+def test_missing_library_raises_at_call_time(monkeypatch, tmp_path):
+    monkeypatch.setattr(_native, "LIB_PATH", tmp_path / "nope.so")
+    monkeypatch.setattr(_native, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        _native.load()
+
+
+def test_check_raises_runtime_error_with_message():
+    with pytest.raises(RuntimeError, match="unsupported dtype"):
+        _native.check(2, "msda_forward")
+
+
+# --- Python boundary validation (reference: tests/test_msda.py:253-269) ---
+
+def _inputs():
+    return make_inputs(B=1, Q=8, M=2, D=16, shapes=[(6, 6)], K=2, dtype=torch.float32, device="cpu")
+
+
+def test_rejects_mismatched_shapes_and_dtypes():
+    value, shapes, starts, loc, attn = _inputs()
+    with pytest.raises(ValueError, match="attention_weights"):
+        multi_scale_deformable_attention(value, shapes, starts, loc, attn[:, :, :, :, :1])
+    with pytest.raises(ValueError, match="dtypes"):
+        multi_scale_deformable_attention(value, shapes, starts, loc.half(), attn)
+    with pytest.raises(ValueError, match="CUDA"):
+        multi_scale_deformable_attention(value, shapes, starts, loc, attn)
+
+
+@pytest.mark.parametrize("mutate,match", [
+    (lambda v, s, st, l, a: (v[0], s, st, l, a), "value must be"),
+    (lambda v, s, st, l, a: (v, s, st, l[..., :1], a), "sampling_locations must be"),
+    (lambda v, s, st, l, a: (v, s, st, l[:, :, :1], a[:, :, :1]), "inconsistent"),
+    (lambda v, s, st, l, a: (v, s[:, :1], st, l, a), "spatial_shapes"),
+    (lambda v, s, st, l, a: (v.double(), s, st, l.double(), a.double()), "unsupported dtype"),
+])
+def test_validation_messages(mutate, match):
+    args = mutate(*_inputs())
+    with pytest.raises(ValueError, match=match):
+        multi_scale_deformable_attention(*args)
+
+
+# --- Presets: published sizes and the reference's byte accounting ---------
+
+@pytest.mark.parametrize("name,S,Q,fwd,bwd", [
+    ("tiny", 1360, 100, 6_809_600, 13_516_800),
+    ("decoder", 22223, 300, 40_857_600, 81_100_800),
+    ("high_contention", 22223, 300, 40_857_600, 81_100_800),
+    ("encoder", 22223, 22223, 1_513_297_408, 3_003_838_464),
+    ("mask2former_fp32", 21504, 21504, 2_207_514_624, 4_370_989_056),
+    ("mask2former_bf16", 21504, 21504, 1_103_757_312, 2_185_494_528),
+])
+def test_preset_sizes_and_bytes(name, S, Q, fwd, bwd):
+    c = presets.preset_dims(name)
+    assert (c["S"], c["Q"]) == (S, Q)
+    assert presets.algorithmic_bytes(name) == (fwd, bwd)
+
+
+def test_decoder_pyramid_matches_reference_shapes():
+    assert presets.pyramid(800, 1333) == [(100, 167), (50, 84), (25, 42), (13, 21)]
+    assert presets.pyramid(1024, 1024, 3) == [(128, 128), (64, 64), (32, 32)]
+
+
+def test_preset_inputs_are_seeded_and_rounded():
+    a = presets.make_preset_inputs("tiny")
+    b = presets.make_preset_inputs("tiny")
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    value, shapes, starts, loc, attn = presets.make_preset_inputs("decoder")
+    assert value.dtype == loc.dtype == attn.dtype == torch.bfloat16
+    assert starts.tolist() == [0, 16700, 20900, 21950]
+    torch.testing.assert_close(attn.float().sum((-1, -2)), torch.ones(4, 300, 8), atol=2e-2, rtol=0)
+    _, _, _, loc_e, _ = presets.make_preset_inputs("encoder")
+    assert loc_e.min() >= -0.1 and loc_e.max() <= 1.1
+
+
+def test_bench_refuses_more_than_one_gpu():
+    res = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=60)
+    assert res.returncode == 2 and "one GPU" in res.stderr
+
+
+def test_graft_entry_points_exist():
+    sys.path.insert(0, str(ROOT))
+    import __graft_entry__ as ge
+
+    assert callable(ge.build) and callable(ge.smoke)

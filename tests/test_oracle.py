@@ -26,7 +26,7 @@ import torch.nn.functional as F
 
 from msda_cases import make_inputs
 from oracle import (level_start_index_of, msda_backward_analytic, msda_naive, msda_reference,
-                    run_reference_fp32)
+                    run_reference, run_reference_fp32)
 
 F64 = torch.float64
 
@@ -378,3 +378,26 @@ def test_run_reference_fp32_protocol():
     ref = msda_reference(value.double(), sh, loc.double(), attn.double())
     torch.testing.assert_close(out.double(), ref, rtol=1e-6, atol=1e-6)
     assert math.isfinite(gv.sum().item())
+
+
+def test_fp32_formula_matches_float64_where_fp32_grid_sample_drifts():
+    """At W = 128 the fp32 grid_sample oracle's grid 2*loc - 1 rounds the
+    image coordinate enough to move grad_loc beyond 1e-4; the kernels' fp32
+    formula x = loc*W - 0.5 (exact for power-of-two W) stays within 1e-4 of
+    the float64 oracle.  This is why fp32 inputs at full size are checked
+    against float64."""
+    gen = torch.Generator().manual_seed(21)
+    shapes = [(128, 128)]
+    B, Q, M, D, K = 1, 512, 2, 32, 4
+    value = torch.randn(B, 128 * 128, M, D, generator=gen)
+    loc = torch.rand(B, Q, M, 1, K, 2, generator=gen) * 0.3  # small locs: 2*loc - 1 rounds
+    attn = torch.rand(B, Q, M, 1, K, generator=gen)
+    g = torch.randn(B, Q, M * D, generator=gen)
+    sh = torch.tensor(shapes)
+    starts = level_start_index_of(sh)
+    _, (_, gl64, _) = run_reference(value, sh, loc, attn, g, dtype=F64)
+    _, (_, gl32, _) = run_reference(value, sh, loc, attn, g, dtype=torch.float32)
+    _, gl_formula, _ = msda_backward_analytic(value, sh, starts, loc, attn, g, dtype=torch.float32)
+    torch.testing.assert_close(gl_formula.double(), gl64, rtol=1e-4, atol=1e-4)
+    drift = (gl32.double() - gl64).abs() / (1 + gl64.abs())
+    assert drift.max() > 1e-4  # the fp32 oracle itself exceeds the fp32 tolerance here
