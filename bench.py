@@ -15,7 +15,8 @@ Prints ONE JSON line:
                accounting, labs/03_the_machine.py:232-251)
   ms_per_step  fwd+bwd wall time per step over the K timed steps
   fwd_us / bwd_us / fwd_gbps ...  per-call device times from HIP events around
-               graph replays of R calls (bwd = zero-fill + backward kernel)
+               graph replays of R calls (bwd = zero-fill + backward kernel);
+               *_cold_us with L2 and Infinity Cache flushed before each call
   roofline     backward pass (the dominant cost) vs 8 TB/s HBM
   roofline_fwd forward kernel vs 8 TB/s HBM (the operator's stated target)
   cpu_baseline the CPU oracle (grid_sample restatement) on the host cores
@@ -108,6 +109,9 @@ def main() -> int:
     ap.add_argument("--fp32-grad-accum", action="store_true",
                     help="accumulate grad_value in an fp32 scratch buffer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-driver", action="store_true",
+                    help="for rocprofv3 --pmc runs: a few eager fwd/bwd calls plus a 256 MiB "
+                         "device copy (counter calibration); prints no JSON")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -159,6 +163,21 @@ def main() -> int:
         fwd()
         bwd()
 
+    if args.pmc_driver:
+        for _ in range(3):
+            step()
+        for _ in range(5):
+            fwd()
+        for _ in range(5):
+            bwd()
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"pmc driver done: {args.preset}, 5 fwd, 5 bwd, 5 copies of {src.numel() * 4} bytes")
+        return 0
+
     def capture(fn, reps):
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream())
@@ -207,6 +226,19 @@ def main() -> int:
     bwd_us = per_call_us(bwd)
     step_us = per_call_us(step, reps=25)
 
+    # Cold variants: a 512 MiB write before every call evicts L2 and the
+    # 256 MiB Infinity Cache, so the inputs come from HBM; the flush's own
+    # time (measured alone) is subtracted.
+    flush_buf = torch.empty(128 << 20, dtype=torch.float32, device=dev)
+
+    def flush():
+        flush_buf.zero_()
+
+    flush_us = per_call_us(flush, reps=10, replays=5)
+    fwd_cold_us = per_call_us(lambda: (flush(), fwd()), reps=10, replays=5) - flush_us
+    bwd_cold_us = per_call_us(lambda: (flush(), bwd()), reps=10, replays=5) - flush_us
+    del flush_buf
+
     # Through the public autograd operator, eagerly (host launch cost included).
     from msda_triton_amd import multi_scale_deformable_attention as msda
 
@@ -216,6 +248,7 @@ def main() -> int:
     g_flat = grad_out.view(B, Q, M * D)
 
     def api_step():
+        v_l.grad = l_l.grad = a_l.grad = None
         o = msda(v_l, shapes, starts, l_l, a_l, fp32_grad_accum=args.fp32_grad_accum)
         o.backward(g_flat)
 
@@ -261,6 +294,8 @@ def main() -> int:
         "fwd_bwd_us": round(step_us, 3),
         "fwd_gbps": round(fwd_gbps, 1),
         "bwd_gbps": round(bwd_gbps, 1),
+        "fwd_cold_us": round(fwd_cold_us, 3),
+        "bwd_cold_us": round(bwd_cold_us, 3),
         "api_eager_fwd_bwd_us": round(api_us, 1),
         "roofline": {
             "bound": "hbm",
