@@ -24,84 +24,13 @@
 // pair, so that one atomic instruction covers four full rows of four
 // different (b, q, m) pairs.
 #include "msda_launch.h"
+#include "msda_scatter.h"
 
 namespace msda {
 
 namespace {
 
 constexpr int kUnroll = 4;
-
-// Scatter of one corner row.  The accumulator row holds D elements of A;
-// seen as 4-byte words (one fp32 element, or a packed pair of fp16 / bf16
-// elements), live chunk lane c of the g_real lanes owns the words
-// c, c + g_real, c + 2 g_real, ...  One atomic instruction then covers
-// g_real consecutive words of every row it touches: the hardware executes
-// buffer atomics per 64-byte segment, so a full segment per instruction is
-// four times faster than the 16-byte pieces a lane's own gather chunk would
-// give.  `sg` holds this lane's grad_out values in that word order.
-template <class T, class A, int CB>
-struct Scatter {
-  static constexpr int kVec = CB / T::kBytes;
-  static constexpr int kWordsPerLane = kVec * A::kBytes / 4;  // 0: odd-D half rows
-  static constexpr int kElemsPerWord = 4 / A::kBytes;
-  static constexpr int kSlots = kWordsPerLane > 0 ? kWordsPerLane * kElemsPerWord : 1;
-
-  // grad_out values of the words this lane scatters.
-  __device__ __forceinline__ static void load_g(const Params& p, int pair, int ch, bool live,
-                                                float (&sg)[kSlots]) {
-    for (int i = 0; i < kSlots; ++i) sg[i] = 0.f;
-    if (!live || pair >= p.npairs) return;
-    const uint64_t base = (uint64_t)pair * (uint32_t)p.D;
-    if constexpr (kWordsPerLane == 0) {
-      sg[0] = load1<T>(p.grad_out, base + ch);  // CB == 2: one element per lane
-    } else {
-#pragma unroll
-      for (int i = 0; i < kWordsPerLane; ++i) {
-        const uint64_t e0 = base + (uint64_t)(ch + p.g_real * i) * kElemsPerWord;
-        if constexpr (kElemsPerWord == 2) {
-          load_xy<T>(p.grad_out, e0 / 2, sg[2 * i], sg[2 * i + 1]);
-        } else {
-          sg[i] = load1<T>(p.grad_out, e0);
-        }
-      }
-    }
-  }
-
-  // Add coef * sg into the row whose accumulator byte offset is `row`
-  // (out-of-range rows are dropped by the buffer range check).
-  __device__ __forceinline__ static void add(__amdgpu_buffer_rsrc_t r, uint32_t row, int ch,
-                                             int g_real, float coef, const float (&sg)[kSlots]) {
-    if constexpr (kWordsPerLane == 0) {
-      // Half storage with odd D: rows are not word aligned; add this lane's
-      // element with the packed atomic on its enclosing word, zero in the
-      // other half.
-      const uint32_t off = row + (uint32_t)ch * A::kBytes;
-      const float v = coef * sg[0];
-      const bool hi = (off & 2u) != 0;
-      if constexpr (A::kCode == kBF16) {
-        bf16x2 x = {(__bf16)(hi ? 0.f : v), (__bf16)(hi ? v : 0.f)};
-        raw_buffer_atomic_fadd_v2bf16(x, r, (int)(off & ~3u), 0, 0);
-      } else {
-        f16x2 x = {(_Float16)(hi ? 0.f : v), (_Float16)(hi ? v : 0.f)};
-        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_v2f16(x, r, (int)(off & ~3u), 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kWordsPerLane; ++i) {
-        const int off = (int)(row + 4u * (uint32_t)(ch + g_real * i));
-        if constexpr (A::kBytes == 4) {
-          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(coef * sg[i], r, off, 0, 0);
-        } else if constexpr (A::kCode == kBF16) {
-          bf16x2 x = {(__bf16)(coef * sg[2 * i]), (__bf16)(coef * sg[2 * i + 1])};
-          raw_buffer_atomic_fadd_v2bf16(x, r, off, 0, 0);
-        } else {
-          f16x2 x = {(_Float16)(coef * sg[2 * i]), (_Float16)(coef * sg[2 * i + 1])};
-          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_v2f16(x, r, off, 0, 0);
-        }
-      }
-    }
-  }
-};
 
 // T: storage dtype.  A: accumulator dtype (F32, or T for in-place atomics).
 template <class T, class A, int CB, int G, int TS>
@@ -114,10 +43,10 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
   constexpr uint32_t kAccScale = A::kBytes / T::kBytes;
 
   __shared__ LevelTable lt;
-  __shared__ uint4 s_off[kMaxRecords];
-  __shared__ float4 s_geo[kMaxRecords];  // lx, ly, A, -
-  __shared__ float2 s_scl[kMaxRecords];  // A*W, A*H
-  __shared__ float4 s_res[kMaxRecords];  // grad_attn, grad_x, grad_y, -
+  __shared__ uint4 s_off[kBwdRecords];
+  __shared__ float4 s_geo[kBwdRecords];  // lx, ly, A, -
+  __shared__ float2 s_scl[kBwdRecords];  // A*W, A*H
+  __shared__ float4 s_res[kBwdRecords];  // grad_attn, grad_x, grad_y, -
 
   const int g = kStatic ? G : p.g_rt;
   const int ts = kStatic ? TS : p.ts_rt;
@@ -213,6 +142,8 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
             const float gy = sc.y * (mx * (d[2] - d[0]) + lx * (d[3] - d[1]));
             s_res[j] = make_float4(ga, gx, gy, 0.f);
           }
+          // Atomics interleaved with the next samples' gathers measured
+          // faster than issuing them all after the gathers (decoder preset).
           if (live) {
             Sc::add(ra, o[u].x * kAccScale, ch, p.g_real, a * w00, sg);
             Sc::add(ra, o[u].y * kAccScale, ch, p.g_real, a * w01, sg);

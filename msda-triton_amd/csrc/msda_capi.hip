@@ -64,11 +64,11 @@ bool choose_shape(int row_bytes, int lk, int64_t npairs, bool backward, int ts_p
   return true;
 }
 
-void finish_params(const Shape& s, Params* p) {
+void finish_params(const Shape& s, int max_records, Params* p) {
   const int team = s.g * s.ts;
   const int ppb = (kWave / team) * (kBlock / kWave);
   int sch = next_pow2(p->LK);
-  if (sch > kMaxRecords / ppb) sch = kMaxRecords / ppb;
+  if (sch > max_records / ppb) sch = max_records / ppb;
   p->sch = sch;
   p->log2_sch = log2i(sch);
   p->npass = (p->LK + sch - 1) / sch;
@@ -83,23 +83,16 @@ static int env_int(const char* name) {
   return v ? atoi(v) : 0;
 }
 
-// Launch-shape overrides for tuning sweeps: slots per pair (power of two).
-static int fwd_ts_pref() {
-  static const int v = env_int("MSDA_FWD_TS");
-  return v;
-}
-static int bwd_ts_pref() {
-  static const int v = env_int("MSDA_BWD_TS");
-  return v;
-}
-// Upper bound on the bytes per lane load (16, 8, 4, 2).
-static int fwd_cb_pref() {
-  static const int v = env_int("MSDA_FWD_CB");
-  return v;
-}
-static int bwd_cb_pref() {
-  static const int v = env_int("MSDA_BWD_CB");
-  return v;
+// Launch-shape overrides (sweeps and tests), read on every call: slots per
+// pair (power of two), upper bound on the bytes per lane load (16, 8, 4, 2),
+// and MSDA_BWD_PRIV=0 to use the direct backward instead of the row-dedup
+// one.  getenv costs well under a microsecond next to the launch.
+static int fwd_ts_pref() { return env_int("MSDA_FWD_TS"); }
+static int bwd_ts_pref() { return env_int("MSDA_BWD_TS"); }
+static int fwd_cb_pref() { return env_int("MSDA_FWD_CB"); }
+static int bwd_cb_pref() { return env_int("MSDA_BWD_CB"); }
+static bool bwd_priv_enabled() {
+  return getenv("MSDA_BWD_PRIV") == nullptr || env_int("MSDA_BWD_PRIV") != 0;
 }
 
 static int elem_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
@@ -198,7 +191,7 @@ extern "C" int msda_forward(const void* value, const int64_t* spatial_shapes,
                                : nullptr;
     p.attn = attention_weights ? at(attention_weights, b0 * d.Q * d.M * d.L * d.K, e) : nullptr;
     p.out = at(output, b0 * d.Q * d.M * d.D, e);
-    finish_params(sh, &p);
+    finish_params(sh, kMaxRecords, &p);
     rc = status(launch_forward(dtype, sh, p, st));
     if (rc != MSDA_OK) return rc;
   }
@@ -261,8 +254,13 @@ extern "C" int msda_backward(const void* value, const int64_t* spatial_shapes,
       p.acc_bytes = (uint32_t)(nb * d.S * d.M * d.D * acc_e);
       p.grad_loc = at(grad_sampling_locations, so * 2, e);
       p.grad_attn = at(grad_attention_weights, so, e);
-      finish_params(sh, &p);
-      rc = status(launch_backward(dtype, fp32_acc, sh, p, st));
+      finish_params(sh, kBwdRecords, &p);
+      if (bwd_priv_enabled() && priv_supported(sh, (int)d.D, (int)d.K, e)) {
+        priv_params(&p);
+        rc = status(launch_backward_priv(dtype, fp32_acc, sh, p, st));
+      } else {
+        rc = status(launch_backward(dtype, fp32_acc, sh, p, st));
+      }
       if (rc != MSDA_OK) return rc;
     }
   }

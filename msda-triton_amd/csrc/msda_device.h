@@ -22,7 +22,8 @@ namespace msda {
 constexpr int kBlock = 256;  // threads per workgroup: 4 wave64
 constexpr int kWave = 64;
 constexpr int kMaxLevels = 64;
-constexpr int kMaxRecords = 512;             // staged samples per workgroup pass
+constexpr int kMaxRecords = 512;             // staged samples per workgroup pass (forward)
+constexpr int kBwdRecords = 256;             // same, backward (keeps LDS for occupancy)
 constexpr uint32_t kOobElem = 1u << 28;      // element-offset sentinel
 constexpr uint32_t kDeadLaneBytes = 1u << 30;  // pushes padding lanes out of range
 constexpr uint32_t kMaxSliceElems = (1u << 28) - 1;
@@ -318,7 +319,9 @@ struct Params {
   int32_t g_real;   // live chunk lanes per value row
   int32_t g_rt;     // runtime G (generic kernels)
   int32_t ts_rt;    // runtime TS (generic kernels)
-  FastDiv div_qm, div_m, div_k;
+  int32_t nq;       // deduplicating backward: queries per workgroup
+  int32_t nqblk;    //   query blocks per (b, m, l)
+  FastDiv div_qm, div_m, div_k, div_d;
 };
 
 // Workgroups are dispatched to the 8 XCDs round-robin (id i -> XCD i % 8).

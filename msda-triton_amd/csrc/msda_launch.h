@@ -26,12 +26,18 @@ FastDiv make_fastdiv(uint32_t d);
 bool choose_shape(int row_bytes, int lk, int64_t npairs, bool backward, int ts_pref,
                   int cb_pref, Shape* out);
 
-// Fills the pass/record fields of `p` for shape `s` (sch, npass, nblocks).
-void finish_params(const Shape& s, Params* p);
+// Fills the pass/record fields of `p` for shape `s` (sch, npass, nblocks)
+// for a kernel that stages at most `max_records` samples per pass.
+void finish_params(const Shape& s, int max_records, Params* p);
 
 hipError_t launch_forward(int dtype, const Shape& s, const Params& p, hipStream_t st);
 hipError_t launch_backward(int dtype, bool fp32_acc, const Shape& s, const Params& p,
                            hipStream_t st);
+// LDS-privatised backward (msda_backward_priv.hip).
+bool priv_supported(const Shape& s, int D, int K, int elem_bytes);
+void priv_params(Params* p);
+hipError_t launch_backward_priv(int dtype, bool fp32_acc, const Shape& s, const Params& p,
+                                hipStream_t st);
 hipError_t launch_zero(void* ptr, uint64_t bytes, hipStream_t st);
 hipError_t launch_cast(int dtype, const float* src, void* dst, uint64_t n, hipStream_t st);
 

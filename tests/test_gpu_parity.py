@@ -192,3 +192,37 @@ def test_backward_loc_and_attn_grads_are_deterministic():
     _, _, g1 = run_fwd_bwd(value, shapes, starts, loc, attn)
     _, _, g2 = run_fwd_bwd(value, shapes, starts, loc, attn)
     assert torch.equal(g1[1], g2[1]) and torch.equal(g1[2], g2[2])
+
+
+# ---------------------------------------------------------------------------
+# Every kernel variant: launch-shape overrides (read by the library per call)
+# ---------------------------------------------------------------------------
+
+OVERRIDES = [
+    dict(),                                          # defaults: dedup backward
+    dict(MSDA_BWD_PRIV="0"),                         # direct backward, 16 lanes/row
+    dict(MSDA_BWD_PRIV="0", MSDA_BWD_CB="16", MSDA_BWD_TS="4"),
+    dict(MSDA_BWD_PRIV="0", MSDA_BWD_CB="8", MSDA_BWD_TS="16"),
+    dict(MSDA_FWD_TS="1"), dict(MSDA_FWD_TS="16"),
+    dict(MSDA_FWD_CB="8", MSDA_FWD_TS="4"), dict(MSDA_FWD_CB="4", MSDA_FWD_TS="2"),
+]
+
+
+@pytest.fixture
+def env_overrides(request, monkeypatch):
+    for k, v in request.param.items():
+        monkeypatch.setenv(k, v)
+    return request.param
+
+
+@pytest.mark.parametrize("env_overrides", OVERRIDES, indirect=True,
+                         ids=lambda d: ",".join(f"{k[5:]}={v}" for k, v in d.items()) or "default")
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("case", [CASES[0], CASES[3]], ids=[CASES[0]["id"], CASES[3]["id"]])
+def test_kernel_variants_match_reference(case, dtype, env_overrides):
+    value, shapes, starts, loc, attn = make_inputs(**case_kwargs(case), dtype=dtype, device=DEVICE,
+                                                   loc_lo=-0.1, loc_hi=1.1)
+    out, g, grads = run_fwd_bwd(value, shapes, starts, loc, attn, fp32_grad_accum=True)
+    ref, refs = run_reference_fp32(value, shapes, loc, attn, g)
+    check_fwd(out, ref, dtype)
+    check_bwd(grads, refs, dtype)

@@ -35,13 +35,18 @@ def _fwd_bwd(name, fp32_grad_accum):
     ("tiny", False),
     ("decoder", False),
     ("decoder", True),
+    ("high_contention", False),
     ("high_contention", True),
     ("encoder", False),
+    ("encoder", True),
     ("mask2former_fp32", False),
     ("mask2former_bf16", False),
     ("mask2former_bf16", True),
 ])
 def test_preset_matches_oracle(name, fp32_grad_accum):
+    """Native-dtype accumulation is part of the contract here, also for the
+    high-contention preset: the backward sums every row's contributions
+    within a workgroup in fp32 and rounds once per (workgroup, row)."""
     dtype = presets.PRESETS[name]["dtype"]
     (value, shapes, loc, attn, g), out, grads = _fwd_bwd(name, fp32_grad_accum)
     # float64 oracle: the fp32 grid_sample grid (2*loc - 1) rounds the image
