@@ -7,5 +7,22 @@ kernels for gfx950 (libmsda_hip.so).
 
 from .ops import multi_scale_deformable_attention
 
-__all__ = ["multi_scale_deformable_attention"]
+__all__ = ["multi_scale_deformable_attention", "msda_op", "MultiScaleDeformableAttnFunction",
+           "MSDeformAttnFunction"]
+
+
+def __getattr__(name):
+    # torch.library registration and the mmcv / Deformable-DETR shims load on
+    # first use, keeping `import msda_triton_amd` as light as the reference's.
+    if name == "msda_op":
+        from .library import msda_op
+
+        return msda_op
+    if name in ("MultiScaleDeformableAttnFunction", "MSDeformAttnFunction"):
+        from . import compat
+
+        return getattr(compat, name)
+    raise AttributeError(name)
+
+
 __version__ = "0.1.0"

@@ -1,0 +1,107 @@
+"""The operator as `torch.library` custom ops: ``torch.ops.msda_amd.forward``
+and ``torch.ops.msda_amd.backward``, with fake (shape) implementations and a
+registered autograd formula.
+
+`multi_scale_deformable_attention` in ops.py mirrors the reference's
+`torch.autograd.Function` (src/msda_triton/ops.py:36-93), which
+`torch.compile` cannot trace into: it graph-breaks around the opaque ctypes
+calls.  Registered custom ops are traceable as single nodes
+(`torch.compile(fullgraph=True)` works), so `msda_op` below is the entry for
+compiled models.  Both entries call the same C ABI (include/msda_hip.h).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native
+from .ops import _DTYPE_CODE, _prepare
+
+
+@torch.library.custom_op("msda_amd::forward", mutates_args=(), device_types="cuda")
+def _forward(value: torch.Tensor, spatial_shapes: torch.Tensor, level_start_index: torch.Tensor,
+             sampling_locations: torch.Tensor, attention_weights: torch.Tensor,
+             fp32_grad_accum: bool) -> torch.Tensor:
+    B, S, M, D = value.shape
+    _, Q, _, L, K, _ = sampling_locations.shape
+    out = value.new_empty(B, Q, M * D)
+    lib = _native.load()
+    with torch.cuda.device(value.device):
+        rc = lib.msda_forward(
+            value.data_ptr(), spatial_shapes.data_ptr(), level_start_index.data_ptr(),
+            sampling_locations.data_ptr(), attention_weights.data_ptr(), out.data_ptr(),
+            B, S, M, D, Q, L, K, _DTYPE_CODE[value.dtype],
+            torch.cuda.current_stream(value.device).cuda_stream)
+    _native.check(rc, "msda_forward")
+    return out
+
+
+@_forward.register_fake
+def _forward_fake(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                  fp32_grad_accum):
+    B, S, M, D = value.shape
+    return value.new_empty(B, sampling_locations.shape[1], M * D)
+
+
+@torch.library.custom_op("msda_amd::backward", mutates_args=(), device_types="cuda")
+def _backward(value: torch.Tensor, spatial_shapes: torch.Tensor, level_start_index: torch.Tensor,
+              sampling_locations: torch.Tensor, attention_weights: torch.Tensor,
+              grad_output: torch.Tensor, fp32_grad_accum: bool
+              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    B, S, M, D = value.shape
+    _, Q, _, L, K, _ = sampling_locations.shape
+    grad_output = grad_output.reshape(B, Q, M, D).contiguous()
+    grad_value = torch.empty_like(value)
+    accum = (torch.empty(value.shape, dtype=torch.float32, device=value.device)
+             if fp32_grad_accum and value.dtype != torch.float32 else None)
+    grad_loc = torch.empty_like(sampling_locations)
+    grad_attn = torch.empty_like(attention_weights)
+    lib = _native.load()
+    with torch.cuda.device(value.device):
+        rc = lib.msda_backward(
+            value.data_ptr(), spatial_shapes.data_ptr(), level_start_index.data_ptr(),
+            sampling_locations.data_ptr(), attention_weights.data_ptr(), grad_output.data_ptr(),
+            grad_value.data_ptr(), None if accum is None else accum.data_ptr(),
+            grad_loc.data_ptr(), grad_attn.data_ptr(), B, S, M, D, Q, L, K,
+            _DTYPE_CODE[value.dtype], torch.cuda.current_stream(value.device).cuda_stream)
+    _native.check(rc, "msda_backward")
+    return grad_value, grad_loc, grad_attn
+
+
+@_backward.register_fake
+def _backward_fake(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                   grad_output, fp32_grad_accum):
+    return (torch.empty_like(value), torch.empty_like(sampling_locations),
+            torch.empty_like(attention_weights))
+
+
+def _setup_context(ctx, inputs, output):
+    value, spatial_shapes, level_start_index, sampling_locations, attention_weights, fp32 = inputs
+    ctx.save_for_backward(value, spatial_shapes, level_start_index, sampling_locations,
+                          attention_weights)
+    ctx.fp32_grad_accum = fp32
+
+
+def _autograd_backward(ctx, grad_out):
+    value, spatial_shapes, level_start_index, sampling_locations, attention_weights = (
+        ctx.saved_tensors)
+    gv, gl, ga = torch.ops.msda_amd.backward(value, spatial_shapes, level_start_index,
+                                             sampling_locations, attention_weights, grad_out,
+                                             ctx.fp32_grad_accum)
+    return gv, None, None, gl, ga, None
+
+
+torch.library.register_autograd("msda_amd::forward", _autograd_backward,
+                                setup_context=_setup_context)
+
+
+def msda_op(value, spatial_shapes, level_start_index, sampling_locations, attention_weights, *,
+            fp32_grad_accum: bool | None = None):
+    """Same contract as `multi_scale_deformable_attention` (validation,
+    defaults, empty-input early return), computed through the registered
+    custom ops so that `torch.compile` captures it as one node."""
+    prep = _prepare(value, spatial_shapes, level_start_index, sampling_locations,
+                    attention_weights, fp32_grad_accum)
+    if isinstance(prep, torch.Tensor):  # B == 0 or Q == 0
+        return prep
+    return torch.ops.msda_amd.forward(*prep)

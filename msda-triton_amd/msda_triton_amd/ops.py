@@ -27,9 +27,11 @@ def _use_fp32_grad_accum(value: torch.Tensor) -> bool:
     21-33, which picks fp32 only where the dtype's atomic add would be an
     emulated compare-and-swap loop).  gfx950 has native fp32, packed-fp16 and
     packed-bf16 global atomics, so the native-dtype path is used for every
-    dtype, as the reference does on SM >= 9.0.  Pass ``fp32_grad_accum=True``
-    when many samples land on the same corners (the native half-precision sum
-    then rounds at every add)."""
+    dtype, as the reference does on SM >= 9.0.  The default (row-dedup)
+    backward sums every row's contributions inside a workgroup in fp32 before
+    its one rounded atomic, which keeps native half-precision accumulation
+    within tolerance even when many samples share corners.  ``True`` still
+    gives a full fp32 accumulation, rounded once."""
     del value
     return False
 
@@ -129,6 +131,18 @@ def multi_scale_deformable_attention(
         ``grad_value`` is accumulated with atomics, so its backward is not
         bitwise deterministic.
     """
+    prep = _prepare(value, spatial_shapes, level_start_index, sampling_locations,
+                    attention_weights, fp32_grad_accum)
+    if isinstance(prep, torch.Tensor):  # B == 0 or Q == 0: no autograd link
+        return prep
+    return _MSDAFunction.apply(*prep)
+
+
+def _prepare(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+             fp32_grad_accum):
+    """Validation and defaults of the operator boundary
+    (src/msda_triton/ops.py:140-199).  Returns the empty output for B == 0 or
+    Q == 0, else the argument tuple of the device computation."""
     if value.dim() != 4:
         raise ValueError(f"value must be (B, S, M, D), got {tuple(value.shape)}")
     if sampling_locations.dim() != 6 or sampling_locations.shape[-1] != 2:
@@ -180,7 +194,7 @@ def multi_scale_deformable_attention(
     if fp32_grad_accum is None:
         fp32_grad_accum = _use_fp32_grad_accum(value)
 
-    return _MSDAFunction.apply(
+    return (
         value.contiguous(),
         spatial_shapes,
         level_start_index,

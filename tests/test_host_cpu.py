@@ -180,3 +180,38 @@ def test_graft_entry_points_exist():
     import __graft_entry__ as ge
 
     assert callable(ge.build) and callable(ge.smoke)
+
+
+# --- torch.library registration and call-site shims (CPU: fake tensors) ---
+
+def test_custom_ops_are_registered_with_fake_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    import msda_triton_amd
+
+    assert callable(msda_triton_amd.msda_op)
+    with FakeTensorMode():
+        value = torch.empty(2, 30, 4, 8)
+        shapes = torch.empty(2, 2, dtype=torch.int64)
+        starts = torch.empty(2, dtype=torch.int64)
+        loc = torch.empty(2, 7, 4, 2, 3, 2)
+        attn = torch.empty(2, 7, 4, 2, 3)
+        out = torch.ops.msda_amd.forward(value, shapes, starts, loc, attn, False)
+        assert out.shape == (2, 7, 32)
+        g = torch.empty(2, 7, 32)
+        gv, gl, ga = torch.ops.msda_amd.backward(value, shapes, starts, loc, attn, g, True)
+        assert gv.shape == value.shape and gl.shape == loc.shape and ga.shape == attn.shape
+
+
+def test_mmcv_shim_signature_and_validation():
+    import inspect
+
+    from msda_triton_amd import MSDeformAttnFunction, MultiScaleDeformableAttnFunction
+
+    assert MSDeformAttnFunction is MultiScaleDeformableAttnFunction
+    params = list(inspect.signature(MultiScaleDeformableAttnFunction.apply).parameters)
+    assert params == ["value", "value_spatial_shapes", "value_level_start_index",
+                      "sampling_locations", "attention_weights", "im2col_step"]
+    value, shapes, starts, loc, attn = _inputs()
+    with pytest.raises(ValueError, match="CUDA"):
+        MultiScaleDeformableAttnFunction.apply(value, shapes, starts, loc, attn, 64)
