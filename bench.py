@@ -19,6 +19,8 @@ Prints ONE JSON line:
                *_cold_us with L2 and Infinity Cache flushed before each call
   roofline     backward pass (the dominant cost) vs 8 TB/s HBM
   roofline_fwd forward kernel vs 8 TB/s HBM (the operator's stated target)
+  other_presets fwd / bwd / fwd+bwd device times and GB/s of the other
+               benchmark presets (encoder, high-contention, Mask2Former, tiny)
   cpu_baseline the CPU oracle (grid_sample restatement) on the host cores
 """
 
@@ -100,6 +102,72 @@ def cpu_baseline(preset: str, max_seconds: float = 25.0) -> dict:
     }
 
 
+def preset_device_times(preset: str, lib, fp32_grad_accum: bool = False, reps: int = 10,
+                        replays: int = 5) -> dict:
+    """fwd / bwd / fwd+bwd device time of one preset: HIP events around
+    replays of a HIP graph holding `reps` back-to-back C-ABI calls."""
+    import torch
+
+    from msda_triton_amd import _native, presets
+    from msda_triton_amd.ops import _DTYPE_CODE
+
+    dev = torch.device("cuda", 0)
+    c = presets.preset_dims(preset)
+    B, S, M, D, Q, L, K = c["B"], c["S"], c["M"], c["D"], c["Q"], c["L"], c["K"]
+    value, shapes, starts, loc, attn = presets.make_preset_inputs(preset, device=dev)
+    grad_out = presets.make_grad_out(preset, device=dev)
+    out = torch.empty(B, Q, M, D, dtype=value.dtype, device=dev)
+    gv, gl, ga = torch.empty_like(value), torch.empty_like(loc), torch.empty_like(attn)
+    accum = (torch.empty(value.shape, dtype=torch.float32, device=dev)
+             if fp32_grad_accum and value.dtype != torch.float32 else None)
+    dt = _DTYPE_CODE[value.dtype]
+    dims = (B, S, M, D, Q, L, K)
+
+    def fwd():
+        _native.check(lib.msda_forward(value.data_ptr(), shapes.data_ptr(), starts.data_ptr(),
+                                       loc.data_ptr(), attn.data_ptr(), out.data_ptr(), *dims, dt,
+                                       torch.cuda.current_stream().cuda_stream), "msda_forward")
+
+    def bwd():
+        _native.check(lib.msda_backward(value.data_ptr(), shapes.data_ptr(), starts.data_ptr(),
+                                        loc.data_ptr(), attn.data_ptr(), grad_out.data_ptr(),
+                                        gv.data_ptr(), None if accum is None else accum.data_ptr(),
+                                        gl.data_ptr(), ga.data_ptr(), *dims, dt,
+                                        torch.cuda.current_stream().cuda_stream), "msda_backward")
+
+    def timed(fn):
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * replays)
+
+    f_us, b_us = timed(fwd), timed(bwd)
+    fb, bb = presets.algorithmic_bytes(preset)
+    return {"fwd_us": round(f_us, 2), "bwd_us": round(b_us, 2), "fwd_bwd_us": round(f_us + b_us, 2),
+            "fwd_gbps": round(fb / f_us / 1e3, 1), "bwd_gbps": round(bb / b_us / 1e3, 1),
+            "fwd_bwd_gbps": round((fb + bb) / (f_us + b_us) / 1e3, 1),
+            "grad_value_accum": "fp32" if accum is not None else str(value.dtype).split(".")[-1]}
+
+
+OTHER_PRESETS = ("tiny", "encoder", "high_contention", "mask2former_fp32", "mask2former_bf16")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description="MSDA fwd+bwd benchmark (one MI355X)")
     ap.add_argument("--gpus", type=int, default=1)
@@ -109,6 +177,8 @@ def main() -> int:
     ap.add_argument("--fp32-grad-accum", action="store_true",
                     help="accumulate grad_value in an fp32 scratch buffer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-presets", action="store_true",
+                    help="skip the device timings of the other presets")
     ap.add_argument("--pmc-driver", action="store_true",
                     help="for rocprofv3 --pmc runs: a few eager fwd/bwd calls plus a 256 MiB "
                          "device copy (counter calibration); prints no JSON")
@@ -319,6 +389,11 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
+    if not args.no_other_presets:
+        record["other_presets"] = {
+            name: preset_device_times(name, lib)
+            for name in OTHER_PRESETS if name != args.preset
+        }
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline(args.preset)
     print(json.dumps(record), flush=True)
