@@ -13,6 +13,10 @@
  *                  (src/msda_triton/ops.py:76-92, kernel at
  *                  src/msda_triton/kernels.py:166-291)
  *
+ * and, one step further out, msda_fused_forward / msda_fused_backward fold
+ * the attention layer's front-end (softmax of the logits, reference point +
+ * offset / (W, H); labs/solutions/lab00.py:194-208) into the same kernels.
+ *
  * Conventions shared by every entry point
  *   - All pointers are device pointers to C-contiguous arrays.
  *   - value                (B, S, M, D)        dtype
@@ -98,6 +102,61 @@ int msda_backward(const void* value, const int64_t* spatial_shapes,
                   int64_t batch, int64_t num_keys, int64_t num_heads,
                   int64_t head_dim, int64_t num_queries, int64_t num_levels,
                   int64_t num_points, int dtype, void* stream);
+
+/*
+ * Fused MSDeformAttn front-end, forward.  Computes what the reference's
+ * attention layer composes in PyTorch around the operator
+ * (labs/solutions/lab00.py:194-208, MSDACrossAttention.forward):
+ *
+ *   weights   = softmax over the L*K points of attention_logits[b,q,m,:]
+ *   locations = reference_points[b,q,(l),:] + sampling_offsets / (W_l, H_l)
+ *   output    = msda_forward(value, ..., locations, weights)
+ *
+ * with the locations and weights formed in the kernel's staging step (fp32),
+ * never stored.  No single reference function corresponds to it: it
+ * replaces the three PyTorch ops of lab00.py:202-207 plus the operator
+ * launch of src/msda_triton/ops.py:46-52.
+ *   reference_points   (B, Q, 2) if reference_levels == 0, or
+ *                      (B, Q, L, 2) if reference_levels == 1; dtype, normalised.
+ *   sampling_offsets   (B, Q, M, L, K, 2) dtype, in level-l pixel units.
+ *   attention_logits   (B, Q, M, L, K)    dtype (softmax over the last two).
+ *   softmax_lse        (B, Q, M) fp32: receives log(sum_{l,k} exp(logit)) of
+ *                      each (b, q, m) for the backward; may be NULL
+ *                      (inference).  Not written when B*Q*M*D == 0.
+ */
+int msda_fused_forward(const void* value, const int64_t* spatial_shapes,
+                       const int64_t* level_start_index, const void* reference_points,
+                       const void* sampling_offsets, const void* attention_logits,
+                       void* output, float* softmax_lse, int64_t batch,
+                       int64_t num_keys, int64_t num_heads, int64_t head_dim,
+                       int64_t num_queries, int64_t num_levels, int64_t num_points,
+                       int reference_levels, int dtype, void* stream);
+
+/*
+ * Fused front-end, backward: gradients of msda_fused_forward.  Replaces the
+ * operator's backward (src/msda_triton/ops.py:76-92) plus the autograd of
+ * lab00.py:202-207 (softmax backward, the division by (W_l, H_l) and the
+ * broadcast sum onto the reference points).
+ *   softmax_lse, output     what msda_fused_forward returned for these inputs.
+ *   grad_value, grad_value_accum  as in msda_backward.
+ *   grad_reference_points   shape of reference_points, written in full; NULL
+ *                           skips it.
+ *   grad_sampling_offsets   (B, Q, M, L, K, 2) dtype, written in full.
+ *   grad_attention_logits   (B, Q, M, L, K)    dtype, written in full.
+ * The softmax backward uses delta = <grad_output, output> per (b, q, m).
+ * All gradients but grad_value are bitwise deterministic.
+ */
+int msda_fused_backward(const void* value, const int64_t* spatial_shapes,
+                        const int64_t* level_start_index, const void* reference_points,
+                        const void* sampling_offsets, const void* attention_logits,
+                        const float* softmax_lse, const void* output,
+                        const void* grad_output, void* grad_value,
+                        float* grad_value_accum, void* grad_reference_points,
+                        void* grad_sampling_offsets, void* grad_attention_logits,
+                        int64_t batch, int64_t num_keys, int64_t num_heads,
+                        int64_t head_dim, int64_t num_queries, int64_t num_levels,
+                        int64_t num_points, int reference_levels, int dtype,
+                        void* stream);
 
 /*
  * Human-readable text for a return code (static storage).  The reference has

@@ -23,6 +23,16 @@
 // value row (4-byte gathers for a 64-byte bf16 row) and one sample slot per
 // pair, so that one atomic instruction covers four full rows of four
 // different (b, q, m) pairs.
+//
+// FUSED = true is the backward of the fused front-end (see msda_forward.hip).
+// A sample's weight is A = softmax(logits)[s] = exp(logit - lse), its location
+// ref + offset / (W, H), so
+//   d/d(logit_s)  = A_s (grad_attn_s - delta),  delta = sum_s' A_s' grad_attn_s'
+//   d/d(offset_s) = grad_loc_s / (W, H)         (the A*W, A*H factors cancel)
+// and delta equals <grad_out[pair], out[pair]> (out = sum_s A_s sampled_s), a
+// per-pair dot that each team computes from the saved forward output -- no
+// reduction over the pair's levels is needed.  Reference points receive the
+// sum of their samples' grad_loc in ref_grad_kernel below.
 #include "msda_launch.h"
 #include "msda_scatter.h"
 
@@ -33,7 +43,7 @@ namespace {
 constexpr int kUnroll = 4;
 
 // T: storage dtype.  A: accumulator dtype (F32, or T for in-place atomics).
-template <class T, class A, int CB, int G, int TS>
+template <class T, class A, int CB, int G, int TS, bool FUSED>
 __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
   using C = Chunk<T, CB>;
   constexpr int kVec = C::kVec;
@@ -78,6 +88,19 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
   using Sc = Scatter<T, A, CB>;
   float sg[Sc::kSlots];
   Sc::load_g(p, pair, ch, live, sg);
+  float delta = 0.f;  // fused: <grad_out, out> of this lane's pair
+  if constexpr (FUSED) {
+    float ov[kVec];
+    C::load(make_rsrc(p.out_fwd, p.gout_bytes),
+            (uint32_t)pair * (uint32_t)(p.D * T::kBytes) + chb, ov);
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) delta += gv[k] * ov[k];
+    if constexpr (kStatic) {
+      delta = xsum_range<1, G / 2, G>(delta);
+    } else {
+      delta = xsum_runtime(delta, 1, g);
+    }
+  }
 
   __syncthreads();
 
@@ -90,8 +113,9 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
       const int jp = j >> p.log2_sch;
       const int s = pass * p.sch + (j & (p.sch - 1));
       const int pr = pair0 + jp;
-      const Sample q = make_sample<T>(p, lt, (uint32_t)pr, (uint32_t)s,
-                                      pr < p.npairs && s < p.LK);
+      const bool valid = pr < p.npairs && s < p.LK;
+      const Sample q = make_sample<T, FUSED>(p, lt, (uint32_t)pr, (uint32_t)s, valid,
+                                             FUSED && valid ? p.lse[pr] : 0.f);
       s_off[j] = make_uint4(q.off[0] * T::kBytes, q.off[1] * T::kBytes, q.off[2] * T::kBytes,
                             q.off[3] * T::kBytes);
       s_geo[j] = make_float4(q.lx, q.ly, q.a, 0.f);
@@ -138,9 +162,13 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
           if (ch == 0) {
             const float2 sc = s_scl[j];
             const float ga = w00 * d[0] + w01 * d[1] + w10 * d[2] + w11 * d[3];
-            const float gx = sc.x * (my * (d[1] - d[0]) + ly * (d[3] - d[2]));
-            const float gy = sc.y * (mx * (d[2] - d[0]) + lx * (d[3] - d[1]));
-            s_res[j] = make_float4(ga, gx, gy, 0.f);
+            const float tx = my * (d[1] - d[0]) + ly * (d[3] - d[2]);
+            const float ty = mx * (d[2] - d[0]) + lx * (d[3] - d[1]);
+            if constexpr (FUSED) {
+              s_res[j] = make_float4(a * (ga - delta), a * tx, a * ty, 0.f);
+            } else {
+              s_res[j] = make_float4(ga, sc.x * tx, sc.y * ty, 0.f);
+            }
           }
           // Atomics interleaved with the next samples' gathers measured
           // faster than issuing them all after the gathers (decoder preset).
@@ -171,30 +199,91 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
   }
 }
 
-template <class T, class A, int CB, int G, int TS>
+template <class T, class A, int CB, int G, int TS, bool FUSED>
 hipError_t launch_one(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((bwd_kernel<T, A, CB, G, TS>), dim3(p.nblocks), dim3(kBlock), 0, st, p);
+  hipLaunchKernelGGL((bwd_kernel<T, A, CB, G, TS, FUSED>), dim3(p.nblocks), dim3(kBlock), 0, st,
+                     p);
   return hipGetLastError();
 }
 
-template <class T, class A>
+template <class T, class A, bool FUSED>
 hipError_t dispatch(const Shape& s, const Params& p, hipStream_t st) {
   switch (s.cb * 10000 + s.g * 100 + s.ts) {
-    case 40801: return launch_one<T, A, 4, 8, 1>(p, st);
-    case 41601: return launch_one<T, A, 4, 16, 1>(p, st);
-    case 41604: return launch_one<T, A, 4, 16, 4>(p, st);
-    case 81601: return launch_one<T, A, 8, 16, 1>(p, st);
-    case 161601: return launch_one<T, A, 16, 16, 1>(p, st);
-    case 160404: return launch_one<T, A, 16, 4, 4>(p, st);
+    case 40801: return launch_one<T, A, 4, 8, 1, FUSED>(p, st);
+    case 41601: return launch_one<T, A, 4, 16, 1, FUSED>(p, st);
+    case 41604: return launch_one<T, A, 4, 16, 4, FUSED>(p, st);
+    case 81601: return launch_one<T, A, 8, 16, 1, FUSED>(p, st);
+    case 161601: return launch_one<T, A, 16, 16, 1, FUSED>(p, st);
+    case 160404: return launch_one<T, A, 16, 4, 4, FUSED>(p, st);
     default: break;
   }
-  if (s.cb == 16) return launch_one<T, A, 16, 0, 0>(p, st);
-  if (s.cb == 8) return launch_one<T, A, 8, 0, 0>(p, st);
-  if (s.cb == 4) return launch_one<T, A, 4, 0, 0>(p, st);
+  if (s.cb == 16) return launch_one<T, A, 16, 0, 0, FUSED>(p, st);
+  if (s.cb == 8) return launch_one<T, A, 8, 0, 0, FUSED>(p, st);
+  if (s.cb == 4) return launch_one<T, A, 4, 0, 0, FUSED>(p, st);
   if constexpr (T::kBytes == 2) {
-    if (s.cb == 2) return launch_one<T, A, 2, 0, 0>(p, st);
+    if (s.cb == 2) return launch_one<T, A, 2, 0, 0, FUSED>(p, st);
   }
   return hipErrorInvalidValue;
+}
+
+template <bool FUSED>
+hipError_t dispatch_dtype(int dtype, bool fp32_acc, const Shape& s, const Params& p,
+                          hipStream_t st) {
+  switch (dtype) {
+    case kF32: return dispatch<F32, F32, FUSED>(s, p, st);
+    case kF16:
+      return fp32_acc ? dispatch<F16, F32, FUSED>(s, p, st) : dispatch<F16, F16, FUSED>(s, p, st);
+    case kBF16:
+      return fp32_acc ? dispatch<BF16, F32, FUSED>(s, p, st)
+                      : dispatch<BF16, BF16, FUSED>(s, p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused front-end: gradient of the reference points.  A reference point
+// moves every location built from it, so its gradient is the sum of those
+// samples' d/d(loc) = (W_l, H_l) * d/d(offset), read back from the offset
+// gradients the backward kernel stored.  One wave per (b, q): lane j covers
+// the (m, k, coordinate) items j, j + 64, ... of one level at a time; since
+// 64 is even a lane always holds the same coordinate (j & 1), and an xor
+// butterfly over lane distances 2..32 (fixed order: deterministic) leaves the
+// x sum in lane 0 and the y sum in lane 1.  Per-level reference points
+// (B,Q,L,2) get one sum per level, shared ones (B,Q,2) one over all levels.
+// ---------------------------------------------------------------------------
+template <class T>
+__global__ __launch_bounds__(kBlock) void ref_grad_kernel(Params p, uint64_t nbq) {
+  __shared__ LevelTable lt;
+  load_levels(p, lt);
+  __syncthreads();
+  const int lane = threadIdx.x % kWave;
+  const uint64_t bq = (uint64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+  if (bq >= nbq) return;  // whole waves
+  const int n = p.M * p.K * 2;
+  float acc = 0.f;
+  for (int l = 0; l < p.L; ++l) {
+    const float sc = (lane & 1) ? (float)lt.h[l] : (float)lt.w[l];
+    for (int j = lane; j < n; j += kWave) {
+      const uint32_t mk = (uint32_t)j >> 1;
+      const uint32_t m = fdiv(mk, p.div_k);
+      const uint32_t k = mk - m * (uint32_t)p.K;
+      const uint64_t e =
+          ((bq * (uint32_t)p.M + m) * (uint32_t)p.LK + (uint32_t)(l * p.K) + k) * 2 + (j & 1);
+      acc += load1<T>(p.grad_loc, e) * sc;
+    }
+    if (p.ref_levels) {
+      float v = acc;
+#pragma unroll
+      for (int d = 2; d < kWave; d <<= 1) v += __shfl_xor(v, d);
+      if (lane < 2) store1<T>(p.grad_ref, (bq * (uint32_t)p.L + l) * 2 + lane, v);
+      acc = 0.f;
+    }
+  }
+  if (!p.ref_levels) {
+#pragma unroll
+    for (int d = 2; d < kWave; d <<= 1) acc += __shfl_xor(acc, d);
+    if (lane < 2) store1<T>(p.grad_ref, bq * 2 + lane, acc);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -232,14 +321,22 @@ int grid_for(uint64_t items) {
 
 }  // namespace
 
-hipError_t launch_backward(int dtype, bool fp32_acc, const Shape& s, const Params& p,
-                           hipStream_t st) {
+hipError_t launch_backward(int dtype, bool fp32_acc, bool fused, const Shape& s,
+                           const Params& p, hipStream_t st) {
+  return fused ? dispatch_dtype<true>(dtype, fp32_acc, s, p, st)
+               : dispatch_dtype<false>(dtype, fp32_acc, s, p, st);
+}
+
+hipError_t launch_ref_grad(int dtype, const Params& p, uint64_t nbq, hipStream_t st) {
+  if (nbq == 0) return hipSuccess;
+  const dim3 grid((unsigned)((nbq + kBlock / kWave - 1) / (kBlock / kWave)));
   switch (dtype) {
-    case kF32: return dispatch<F32, F32>(s, p, st);
-    case kF16: return fp32_acc ? dispatch<F16, F32>(s, p, st) : dispatch<F16, F16>(s, p, st);
-    case kBF16: return fp32_acc ? dispatch<BF16, F32>(s, p, st) : dispatch<BF16, BF16>(s, p, st);
+    case kF32: hipLaunchKernelGGL(ref_grad_kernel<F32>, grid, dim3(kBlock), 0, st, p, nbq); break;
+    case kF16: hipLaunchKernelGGL(ref_grad_kernel<F16>, grid, dim3(kBlock), 0, st, p, nbq); break;
+    case kBF16: hipLaunchKernelGGL(ref_grad_kernel<BF16>, grid, dim3(kBlock), 0, st, p, nbq); break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
 }
 
 hipError_t launch_zero(void* ptr, uint64_t bytes, hipStream_t st) {

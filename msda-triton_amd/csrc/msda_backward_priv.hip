@@ -27,6 +27,12 @@
 // Query blocks of one head sample nearby pixels in encoder-style
 // self-attention (Q = S, reference points on the pixel grid) and when
 // sampling is concentrated, so those cases see the largest reduction.
+//
+// FUSED = true: backward of the fused front-end (formulas in
+// msda_backward.hip).  The block holds one level of each pair, but the
+// softmax couples all L*K samples; the coupling enters only through
+// delta = <grad_out, out>, which each block computes for its queries from the
+// staged grad_out rows and the saved forward output.
 #include "msda_launch.h"
 #include "msda_scatter.h"
 
@@ -66,7 +72,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* warp_sums, int* 
   return base + x - v;
 }
 
-template <class T, class A, int CB, int G>
+template <class T, class A, int CB, int G, bool FUSED>
 __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
   using C = Chunk<T, CB>;
   using Sc = Scatter<T, A, CB>;
@@ -91,6 +97,7 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
   __shared__ uint16_t s_csr[kEntries];
   __shared__ uint16_t s_multi[kEntries];  // rows with >= 2 entries
   __shared__ float s_g[kGFloats];
+  __shared__ float s_delta[FUSED ? kPrivSamples : 1];  // fused: <grad_out, out> per query
   __shared__ int s_wsum[4];
   __shared__ int n_multi;
   __shared__ LevelTable lt;
@@ -155,7 +162,8 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
     const int q = q0 + qi;
     const bool valid = si < ns && q < p.Q;
     const uint32_t pair = (uint32_t)(((int64_t)b * p.Q + q) * p.M + m);
-    const Sample smp = make_sample<T>(p, lt, valid ? pair : 0u, (uint32_t)(l * K + k), valid);
+    const Sample smp = make_sample<T, FUSED>(p, lt, valid ? pair : 0u, (uint32_t)(l * K + k),
+                                             valid, FUSED && valid ? p.lse[pair] : 0.f);
     if (half == 0) {
       s_off[si] = make_uint4(smp.off[0] * T::kBytes, smp.off[1] * T::kBytes,
                              smp.off[2] * T::kBytes, smp.off[3] * T::kBytes);
@@ -178,6 +186,27 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
         pos = (uint16_t)h;
       }
       s_pos[4 * si + c] = pos;
+    }
+  }
+  if constexpr (FUSED) {
+    // delta per query: tq lanes (a power of two <= 64) per query, strided
+    // over the D channels, merged by an xor butterfly (deterministic order).
+    int nqp = 1;
+    while (nqp < nq) nqp <<= 1;
+    const int tq = kBlock / nqp < kWave ? kBlock / nqp : kWave;
+    const int sub = tid % tq;
+    for (int qb = 0; qb < nq; qb += kBlock / tq) {
+      const int qi = qb + tid / tq;
+      const int q = q0 + qi;
+      float acc = 0.f;
+      if (qi < nq && q < p.Q) {
+        const uint64_t pair = ((uint64_t)b * (uint32_t)p.Q + (uint32_t)q) * (uint32_t)p.M + m;
+        for (int d = sub; d < D; d += tq) {
+          acc += s_g[qi * D + d] * load1<T>(p.out_fwd, pair * (uint32_t)D + d);
+        }
+      }
+      for (int x = 1; x < tq; x <<= 1) acc += __shfl_xor(acc, x);
+      if (sub == 0 && qi < nq) s_delta[qi] = acc;
     }
   }
   __syncthreads();
@@ -258,9 +287,13 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
         const float mx = 1.f - lx, my = 1.f - ly;
         if (ch == 0) {
           const float ga = mx * my * d[0] + lx * my * d[1] + mx * ly * d[2] + lx * ly * d[3];
-          const float gx = a * fw * (my * (d[1] - d[0]) + ly * (d[3] - d[2]));
-          const float gy = a * fh * (mx * (d[2] - d[0]) + lx * (d[3] - d[1]));
-          s_res[s] = make_float4(ga, gx, gy, 0.f);
+          const float tx = my * (d[1] - d[0]) + ly * (d[3] - d[2]);
+          const float ty = mx * (d[2] - d[0]) + lx * (d[3] - d[1]);
+          if constexpr (FUSED) {
+            s_res[s] = make_float4(a * (ga - s_delta[qi]), a * tx, a * ty, 0.f);
+          } else {
+            s_res[s] = make_float4(ga, a * fw * tx, a * fh * ty, 0.f);
+          }
         }
         if (live) {
           float sg[Sc::kSlots];
@@ -351,19 +384,34 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
   }
 }
 
-template <class T, class A, int CB, int G>
+template <class T, class A, int CB, int G, bool FUSED>
 hipError_t launch_one(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((bwd_priv_kernel<T, A, CB, G>), dim3(p.nblocks), dim3(kBlock), 0, st, p);
+  hipLaunchKernelGGL((bwd_priv_kernel<T, A, CB, G, FUSED>), dim3(p.nblocks), dim3(kBlock), 0, st,
+                     p);
   return hipGetLastError();
 }
 
-template <class T, class A>
+template <class T, class A, bool FUSED>
 hipError_t dispatch(const Shape& s, const Params& p, hipStream_t st) {
   switch (s.cb * 100 + s.g) {
-    case 408: return launch_one<T, A, 4, 8>(p, st);
-    case 416: return launch_one<T, A, 4, 16>(p, st);
-    case 816: return launch_one<T, A, 8, 16>(p, st);
-    case 1616: return launch_one<T, A, 16, 16>(p, st);
+    case 408: return launch_one<T, A, 4, 8, FUSED>(p, st);
+    case 416: return launch_one<T, A, 4, 16, FUSED>(p, st);
+    case 816: return launch_one<T, A, 8, 16, FUSED>(p, st);
+    case 1616: return launch_one<T, A, 16, 16, FUSED>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <bool FUSED>
+hipError_t dispatch_dtype(int dtype, bool fp32_acc, const Shape& s, const Params& p,
+                          hipStream_t st) {
+  switch (dtype) {
+    case kF32: return dispatch<F32, F32, FUSED>(s, p, st);
+    case kF16:
+      return fp32_acc ? dispatch<F16, F32, FUSED>(s, p, st) : dispatch<F16, F16, FUSED>(s, p, st);
+    case kBF16:
+      return fp32_acc ? dispatch<BF16, F32, FUSED>(s, p, st)
+                      : dispatch<BF16, BF16, FUSED>(s, p, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -387,14 +435,10 @@ void priv_params(Params* p) {
   p->nblocks = (p->npairs / (p->Q > 0 ? p->Q : 1)) * p->L * p->nqblk;
 }
 
-hipError_t launch_backward_priv(int dtype, bool fp32_acc, const Shape& s, const Params& p,
-                                hipStream_t st) {
-  switch (dtype) {
-    case kF32: return dispatch<F32, F32>(s, p, st);
-    case kF16: return fp32_acc ? dispatch<F16, F32>(s, p, st) : dispatch<F16, F16>(s, p, st);
-    case kBF16: return fp32_acc ? dispatch<BF16, F32>(s, p, st) : dispatch<BF16, BF16>(s, p, st);
-    default: return hipErrorInvalidValue;
-  }
+hipError_t launch_backward_priv(int dtype, bool fp32_acc, bool fused, const Shape& s,
+                                const Params& p, hipStream_t st) {
+  return fused ? dispatch_dtype<true>(dtype, fp32_acc, s, p, st)
+               : dispatch_dtype<false>(dtype, fp32_acc, s, p, st);
 }
 
 }  // namespace msda

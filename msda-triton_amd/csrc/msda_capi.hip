@@ -152,6 +152,156 @@ static const char* at(const void* base, int64_t elems, int e) {
 }
 static char* at(void* base, int64_t elems, int e) { return static_cast<char*>(base) + elems * e; }
 
+// Fused front-end arguments (NULL when the call takes locations + weights).
+struct FusedArgs {
+  const void* ref;     // reference points
+  float* lse;          // forward: output (may be NULL); backward: input
+  const void* output;  // backward: the forward output
+  void* grad_ref;      // backward: may be NULL
+  int ref_levels;      // 0: (B, Q, 2); 1: (B, Q, L, 2)
+};
+
+static int forward_impl(const void* value, const int64_t* spatial_shapes,
+                        const int64_t* level_start_index, const void* loc, const void* attn,
+                        void* output, const Dims& d, int dtype, void* stream,
+                        const FusedArgs* f) {
+  int rc = check_dims(d, dtype);
+  if (rc != MSDA_OK) return rc;
+  const int64_t n_out = d.B * d.Q * d.M * d.D;
+  if (n_out == 0) return MSDA_OK;
+  const int64_t n_smp = d.B * d.Q * d.M * d.L * d.K;
+  if (!output || (d.L > 0 && (!spatial_shapes || !level_start_index)) ||
+      (n_smp > 0 && (!loc || !attn || (f && !f->ref))) || (d.B * d.S * d.M * d.D > 0 && !value))
+    return MSDA_ERR_INVALID_ARGUMENT;
+  const int e = elem_bytes(dtype);
+  Shape sh;
+  if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, false, fwd_ts_pref(),
+                    fwd_cb_pref(), &sh))
+    return MSDA_ERR_UNSUPPORTED_SHAPE;
+  const int64_t bs = slice_batch(d);
+  if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t ref_per_b = d.Q * (f && f->ref_levels ? d.L : 1) * 2;
+  for (int64_t b0 = 0; b0 < d.B; b0 += bs) {
+    const int64_t nb = d.B - b0 < bs ? d.B - b0 : bs;
+    Params p = {};
+    base_params(d, b0, nb, dtype, &p);
+    const int64_t so = b0 * d.Q * d.M * d.L * d.K;
+    p.value = value ? at(value, b0 * d.S * d.M * d.D, e) : nullptr;
+    p.shapes = spatial_shapes;
+    p.starts = level_start_index;
+    p.loc = loc ? at(loc, so * 2, e) : nullptr;
+    p.attn = attn ? at(attn, so, e) : nullptr;
+    p.out = at(output, b0 * d.Q * d.M * d.D, e);
+    if (f) {
+      p.ref = f->ref ? at(f->ref, b0 * ref_per_b, e) : nullptr;
+      p.lse = f->lse ? f->lse + b0 * d.Q * d.M : nullptr;
+      p.ref_levels = f->ref_levels;
+    }
+    finish_params(sh, kMaxRecords, &p);
+    rc = status(launch_forward(dtype, f != nullptr, sh, p, st));
+    if (rc != MSDA_OK) return rc;
+  }
+  return MSDA_OK;
+}
+
+static int backward_impl(const void* value, const int64_t* spatial_shapes,
+                         const int64_t* level_start_index, const void* loc, const void* attn,
+                         const void* grad_output, void* grad_value, float* grad_value_accum,
+                         void* grad_loc, void* grad_attn, const Dims& d, int dtype, void* stream,
+                         const FusedArgs* f) {
+  int rc = check_dims(d, dtype);
+  if (rc != MSDA_OK) return rc;
+  const int e = elem_bytes(dtype);
+  const int64_t n_val = d.B * d.S * d.M * d.D;
+  const int64_t n_smp = d.B * d.Q * d.M * d.L * d.K;
+  const int64_t n_out = d.B * d.Q * d.M * d.D;
+  if ((n_val > 0 && (!value || !grad_value)) ||
+      (n_smp > 0 && (!loc || !attn || !grad_loc || !grad_attn)) ||
+      (n_out > 0 && !grad_output) || (d.L > 0 && (!spatial_shapes || !level_start_index)))
+    return MSDA_ERR_INVALID_ARGUMENT;
+  if (f && n_smp > 0 && n_out > 0 && d.S > 0 && (!f->ref || !f->lse || !f->output))
+    return MSDA_ERR_INVALID_ARGUMENT;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // fp32 accumulation is only a separate path for half storage.
+  const bool fp32_acc = grad_value_accum != nullptr && dtype != kF32 && n_val > 0;
+  void* acc = fp32_acc ? static_cast<void*>(grad_value_accum) : grad_value;
+  const int acc_e = fp32_acc ? 4 : e;
+
+  rc = status(launch_zero(acc, (uint64_t)(n_val * acc_e), st));
+  if (rc != MSDA_OK) return rc;
+  const bool compute = n_smp > 0 && n_out > 0 && d.S > 0;
+  if (n_smp > 0 && !compute) {
+    // No channels or no keys: every sampled value is zero, so are the
+    // location and weight gradients (and, fused, the offset, logit and
+    // reference-point gradients: delta = <grad_out, 0> = 0).
+    rc = status(launch_zero(grad_loc, (uint64_t)(n_smp * 2 * e), st));
+    if (rc == MSDA_OK) rc = status(launch_zero(grad_attn, (uint64_t)(n_smp * e), st));
+    if (rc != MSDA_OK) return rc;
+  } else if (compute) {
+    Shape sh;
+    if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, true, bwd_ts_pref(),
+                      bwd_cb_pref(), &sh))
+      return MSDA_ERR_UNSUPPORTED_SHAPE;
+    const int64_t bs = slice_batch(d);
+    if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
+    const int64_t ref_per_b = d.Q * (f && f->ref_levels ? d.L : 1) * 2;
+    for (int64_t b0 = 0; b0 < d.B; b0 += bs) {
+      const int64_t nb = d.B - b0 < bs ? d.B - b0 : bs;
+      Params p = {};
+      base_params(d, b0, nb, dtype, &p);
+      const int64_t vo = b0 * d.S * d.M * d.D, so = b0 * d.Q * d.M * d.L * d.K;
+      const int64_t oo = b0 * d.Q * d.M * d.D;
+      p.value = at(value, vo, e);
+      p.shapes = spatial_shapes;
+      p.starts = level_start_index;
+      p.loc = at(loc, so * 2, e);
+      p.attn = at(attn, so, e);
+      p.grad_out = at(grad_output, oo, e);
+      p.grad_acc = at(acc, vo, acc_e);
+      p.acc_bytes = (uint32_t)(nb * d.S * d.M * d.D * acc_e);
+      p.grad_loc = at(grad_loc, so * 2, e);
+      p.grad_attn = at(grad_attn, so, e);
+      if (f) {
+        p.ref = at(f->ref, b0 * ref_per_b, e);
+        p.lse = f->lse + b0 * d.Q * d.M;
+        p.out_fwd = at(f->output, oo, e);
+        p.ref_levels = f->ref_levels;
+      }
+      finish_params(sh, kBwdRecords, &p);
+      if (bwd_priv_enabled() && priv_supported(sh, (int)d.D, (int)d.K, e)) {
+        priv_params(&p);
+        rc = status(launch_backward_priv(dtype, fp32_acc, f != nullptr, sh, p, st));
+      } else {
+        rc = status(launch_backward(dtype, fp32_acc, f != nullptr, sh, p, st));
+      }
+      if (rc != MSDA_OK) return rc;
+    }
+  }
+  if (fp32_acc) {
+    rc = status(launch_cast(dtype, grad_value_accum, grad_value, (uint64_t)n_val, st));
+    if (rc != MSDA_OK) return rc;
+  }
+  if (f && f->grad_ref) {
+    const int64_t nbq = d.B * d.Q;
+    if (compute) {
+      Params p = {};
+      base_params(d, 0, d.B, dtype, &p);
+      p.shapes = spatial_shapes;
+      p.starts = level_start_index;
+      p.grad_loc = grad_loc;
+      p.grad_ref = f->grad_ref;
+      p.ref_levels = f->ref_levels;
+      rc = status(launch_ref_grad(dtype, p, (uint64_t)nbq, st));
+    } else {
+      rc = status(launch_zero(f->grad_ref,
+                              (uint64_t)(nbq * (f->ref_levels ? d.L : 1) * 2 * e), st));
+    }
+    if (rc != MSDA_OK) return rc;
+  }
+  return MSDA_OK;
+}
+
 }  // namespace msda
 
 using namespace msda;
@@ -163,39 +313,8 @@ extern "C" int msda_forward(const void* value, const int64_t* spatial_shapes,
                             int64_t num_queries, int64_t num_levels, int64_t num_points,
                             int dtype, void* stream) {
   const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
-  int rc = check_dims(d, dtype);
-  if (rc != MSDA_OK) return rc;
-  const int64_t n_out = d.B * d.Q * d.M * d.D;
-  if (n_out == 0) return MSDA_OK;
-  const int64_t n_smp = d.B * d.Q * d.M * d.L * d.K;
-  if (!output || (d.L > 0 && (!spatial_shapes || !level_start_index)) ||
-      (n_smp > 0 && (!sampling_locations || !attention_weights)) ||
-      (d.B * d.S * d.M * d.D > 0 && !value))
-    return MSDA_ERR_INVALID_ARGUMENT;
-  const int e = elem_bytes(dtype);
-  Shape sh;
-  if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, false, fwd_ts_pref(),
-                    fwd_cb_pref(), &sh))
-    return MSDA_ERR_UNSUPPORTED_SHAPE;
-  const int64_t bs = slice_batch(d);
-  if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  for (int64_t b0 = 0; b0 < d.B; b0 += bs) {
-    const int64_t nb = d.B - b0 < bs ? d.B - b0 : bs;
-    Params p = {};
-    base_params(d, b0, nb, dtype, &p);
-    p.value = value ? at(value, b0 * d.S * d.M * d.D, e) : nullptr;
-    p.shapes = spatial_shapes;
-    p.starts = level_start_index;
-    p.loc = sampling_locations ? at(sampling_locations, b0 * d.Q * d.M * d.L * d.K * 2, e)
-                               : nullptr;
-    p.attn = attention_weights ? at(attention_weights, b0 * d.Q * d.M * d.L * d.K, e) : nullptr;
-    p.out = at(output, b0 * d.Q * d.M * d.D, e);
-    finish_params(sh, kMaxRecords, &p);
-    rc = status(launch_forward(dtype, sh, p, st));
-    if (rc != MSDA_OK) return rc;
-  }
-  return MSDA_OK;
+  return forward_impl(value, spatial_shapes, level_start_index, sampling_locations,
+                      attention_weights, output, d, dtype, stream, nullptr);
 }
 
 extern "C" int msda_backward(const void* value, const int64_t* spatial_shapes,
@@ -207,68 +326,44 @@ extern "C" int msda_backward(const void* value, const int64_t* spatial_shapes,
                              int64_t head_dim, int64_t num_queries, int64_t num_levels,
                              int64_t num_points, int dtype, void* stream) {
   const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
-  int rc = check_dims(d, dtype);
-  if (rc != MSDA_OK) return rc;
-  const int e = elem_bytes(dtype);
-  const int64_t n_val = d.B * d.S * d.M * d.D;
-  const int64_t n_smp = d.B * d.Q * d.M * d.L * d.K;
-  const int64_t n_out = d.B * d.Q * d.M * d.D;
-  if ((n_val > 0 && (!value || !grad_value)) ||
-      (n_smp > 0 && (!sampling_locations || !attention_weights || !grad_sampling_locations ||
-                     !grad_attention_weights)) ||
-      (n_out > 0 && !grad_output) || (d.L > 0 && (!spatial_shapes || !level_start_index)))
-    return MSDA_ERR_INVALID_ARGUMENT;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  // fp32 accumulation is only a separate path for half storage.
-  const bool fp32_acc = grad_value_accum != nullptr && dtype != kF32 && n_val > 0;
-  void* acc = fp32_acc ? static_cast<void*>(grad_value_accum) : grad_value;
-  const int acc_e = fp32_acc ? 4 : e;
+  return backward_impl(value, spatial_shapes, level_start_index, sampling_locations,
+                       attention_weights, grad_output, grad_value, grad_value_accum,
+                       grad_sampling_locations, grad_attention_weights, d, dtype, stream,
+                       nullptr);
+}
 
-  rc = status(launch_zero(acc, (uint64_t)(n_val * acc_e), st));
-  if (rc != MSDA_OK) return rc;
-  if (n_smp > 0 && (n_out == 0 || d.S == 0)) {
-    // No channels or no keys: every sampled value is zero, so are the
-    // location and weight gradients.
-    rc = status(launch_zero(grad_sampling_locations, (uint64_t)(n_smp * 2 * e), st));
-    if (rc == MSDA_OK) rc = status(launch_zero(grad_attention_weights, (uint64_t)(n_smp * e), st));
-    if (rc != MSDA_OK) return rc;
-  } else if (n_smp > 0) {
-    Shape sh;
-    if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, true, bwd_ts_pref(),
-                      bwd_cb_pref(), &sh))
-      return MSDA_ERR_UNSUPPORTED_SHAPE;
-    const int64_t bs = slice_batch(d);
-    if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
-    for (int64_t b0 = 0; b0 < d.B; b0 += bs) {
-      const int64_t nb = d.B - b0 < bs ? d.B - b0 : bs;
-      Params p = {};
-      base_params(d, b0, nb, dtype, &p);
-      const int64_t vo = b0 * d.S * d.M * d.D, so = b0 * d.Q * d.M * d.L * d.K;
-      p.value = at(value, vo, e);
-      p.shapes = spatial_shapes;
-      p.starts = level_start_index;
-      p.loc = at(sampling_locations, so * 2, e);
-      p.attn = at(attention_weights, so, e);
-      p.grad_out = at(grad_output, b0 * d.Q * d.M * d.D, e);
-      p.grad_acc = at(acc, vo, acc_e);
-      p.acc_bytes = (uint32_t)(nb * d.S * d.M * d.D * acc_e);
-      p.grad_loc = at(grad_sampling_locations, so * 2, e);
-      p.grad_attn = at(grad_attention_weights, so, e);
-      finish_params(sh, kBwdRecords, &p);
-      if (bwd_priv_enabled() && priv_supported(sh, (int)d.D, (int)d.K, e)) {
-        priv_params(&p);
-        rc = status(launch_backward_priv(dtype, fp32_acc, sh, p, st));
-      } else {
-        rc = status(launch_backward(dtype, fp32_acc, sh, p, st));
-      }
-      if (rc != MSDA_OK) return rc;
-    }
-  }
-  if (fp32_acc) {
-    rc = status(launch_cast(dtype, grad_value_accum, grad_value, (uint64_t)n_val, st));
-    if (rc != MSDA_OK) return rc;
-  }
-  return MSDA_OK;
+extern "C" int msda_fused_forward(const void* value, const int64_t* spatial_shapes,
+                                  const int64_t* level_start_index, const void* reference_points,
+                                  const void* sampling_offsets, const void* attention_logits,
+                                  void* output, float* softmax_lse, int64_t batch,
+                                  int64_t num_keys, int64_t num_heads, int64_t head_dim,
+                                  int64_t num_queries, int64_t num_levels, int64_t num_points,
+                                  int reference_levels, int dtype, void* stream) {
+  if (reference_levels != 0 && reference_levels != 1) return MSDA_ERR_INVALID_ARGUMENT;
+  const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
+  const FusedArgs f{reference_points, softmax_lse, nullptr, nullptr, reference_levels};
+  return forward_impl(value, spatial_shapes, level_start_index, sampling_offsets,
+                      attention_logits, output, d, dtype, stream, &f);
+}
+
+extern "C" int msda_fused_backward(const void* value, const int64_t* spatial_shapes,
+                                   const int64_t* level_start_index, const void* reference_points,
+                                   const void* sampling_offsets, const void* attention_logits,
+                                   const float* softmax_lse, const void* output,
+                                   const void* grad_output, void* grad_value,
+                                   float* grad_value_accum, void* grad_reference_points,
+                                   void* grad_sampling_offsets, void* grad_attention_logits,
+                                   int64_t batch, int64_t num_keys, int64_t num_heads,
+                                   int64_t head_dim, int64_t num_queries, int64_t num_levels,
+                                   int64_t num_points, int reference_levels, int dtype,
+                                   void* stream) {
+  if (reference_levels != 0 && reference_levels != 1) return MSDA_ERR_INVALID_ARGUMENT;
+  const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
+  const FusedArgs f{reference_points, const_cast<float*>(softmax_lse), output,
+                    grad_reference_points, reference_levels};
+  return backward_impl(value, spatial_shapes, level_start_index, sampling_offsets,
+                       attention_logits, grad_output, grad_value, grad_value_accum,
+                       grad_sampling_offsets, grad_attention_logits, d, dtype, stream, &f);
 }
 
 extern "C" const char* msda_error_string(int code) {
@@ -284,4 +379,4 @@ extern "C" const char* msda_error_string(int code) {
   }
 }
 
-extern "C" int msda_abi_version(void) { return (1 << 16) | 0; }
+extern "C" int msda_abi_version(void) { return (1 << 16) | 1; }

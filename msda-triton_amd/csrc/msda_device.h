@@ -295,17 +295,28 @@ __device__ __forceinline__ float xsum_runtime(float v, int first, int end) {
 // --------------------------------------------------------------------------
 // Kernel parameters (by value).  One launch covers a batch slice.
 // --------------------------------------------------------------------------
+//
+// Fused front-end (kernels instantiated with FUSED = true): `loc` holds the
+// sampling offsets in each level's pixel units and `attn` the attention
+// logits; a sample's location is ref + offset / (W_l, H_l) and its weight
+// softmax over the pair's L*K logits, exp(logit - lse[pair]).  The backward
+// then writes d/d(offset) into grad_loc and d/d(logit) into grad_attn.
 struct Params {
   const void* value;
   const int64_t* shapes;
   const int64_t* starts;
-  const void* loc;
-  const void* attn;
+  const void* loc;       // sampling locations (fused: sampling offsets)
+  const void* attn;      // attention weights (fused: attention logits)
   void* out;             // forward output
   const void* grad_out;  // backward
   void* grad_acc;        // backward atomic target (grad_value or fp32 scratch)
-  void* grad_loc;
-  void* grad_attn;
+  void* grad_loc;        // fused: grad of the offsets
+  void* grad_attn;       // fused: grad of the logits
+  const void* ref;       // fused: reference points (B,Q,2) or (B,Q,L,2)
+  float* lse;            // fused: per-pair log-sum-exp of the logits (B,Q,M)
+  const void* out_fwd;   // fused backward: the forward output (for <g, out>)
+  void* grad_ref;        // fused backward: grad of the reference points
+  int32_t ref_levels;    // fused: 1 if reference points are per level
   uint32_t value_bytes;  // num_records of the value buffer
   uint32_t acc_bytes;    // num_records of the accumulator buffer
   uint32_t gout_bytes;   // num_records of grad_out
@@ -349,6 +360,48 @@ __device__ __forceinline__ void load_levels(const Params& p, LevelTable& t) {
   }
 }
 
+// Fused front-end: log-sum-exp of the L*K logits of each of the workgroup's
+// `ppb` pairs (pair0, pair0 + 1, ...) into s_lse[0..ppb) and, when p.lse is
+// set, into p.lse.  `tpp` lanes (a power of two <= 64) share a pair: each
+// keeps a running (max, sum of exp(x - max)) over a strided subset of the
+// logits, then the lanes are merged by an xor butterfly in a fixed order, so
+// the result does not depend on scheduling.  Every thread of the workgroup
+// must call it (cross-lane exchanges).
+template <class T>
+__device__ __forceinline__ void pair_lse(const Params& p, int pair0, int ppb, int tpp,
+                                         float* s_lse) {
+  const int per_iter = kBlock / tpp;
+  const int sub = threadIdx.x % tpp;
+  for (int base = 0; base < ppb; base += per_iter) {
+    const int jp = base + (int)threadIdx.x / tpp;
+    const int pr = pair0 + jp;
+    float mx = -INFINITY, z = 0.f;
+    if (jp < ppb && pr < p.npairs) {
+      const uint64_t i0 = (uint64_t)pr * (uint32_t)p.LK;
+      for (int s = sub; s < p.LK; s += tpp) {
+        const float x = load1<T>(p.attn, i0 + s);
+        if (x > mx) {
+          z = z * expf(mx - x) + 1.f;
+          mx = x;
+        } else {
+          z += expf(x - mx);
+        }
+      }
+    }
+    for (int d = 1; d < tpp; d <<= 1) {
+      const float mo = __shfl_xor(mx, d), zo = __shfl_xor(z, d);
+      const float mn = fmaxf(mx, mo);
+      z = mn == -INFINITY ? 0.f : z * expf(mx - mn) + zo * expf(mo - mn);
+      mx = mn;
+    }
+    if (sub == 0 && jp < ppb) {
+      const float lse = mx + logf(z);
+      s_lse[jp] = lse;
+      if (p.lse != nullptr && pr < p.npairs) p.lse[pr] = lse;
+    }
+  }
+}
+
 // Bilinear geometry of one sample (pair, s), shared by both directions.
 // Coordinates follow x = loc_x * W - 0.5 (src/msda_triton/kernels.py:112-128),
 // evaluated without contraction so that it rounds like grid_sample's
@@ -358,26 +411,45 @@ struct Sample {
   float lx, ly, a, fw, fh;
 };
 
-template <class T>
+//
+// FUSED: the location is ref + offset / (W, H) (labs/solutions/lab00.py:
+// 201-207), i.e. the image coordinate x = ref_x * W + offset_x - 0.5, which
+// is evaluated in that form: one fma, exact for half-precision inputs of the
+// usual magnitudes (so bilinear cells match exact arithmetic even at
+// knots), and no division.  The weight is exp(logit - lse), `lse` being the
+// pair's log-sum-exp.
+template <class T, bool FUSED = false>
 __device__ __forceinline__ Sample make_sample(const Params& p, const LevelTable& lt,
-                                              uint32_t pair, uint32_t s, bool valid) {
+                                              uint32_t pair, uint32_t s, bool valid,
+                                              float lse = 0.f) {
   Sample r;
   if (!valid) {
     r.off[0] = r.off[1] = r.off[2] = r.off[3] = kOobElem;
     r.lx = r.ly = r.a = r.fw = r.fh = 0.f;
     return r;
   }
+  const uint32_t bq = fdiv(pair, p.div_m);
   const uint32_t b = fdiv(pair, p.div_qm);
-  const uint32_t m = pair - fdiv(pair, p.div_m) * (uint32_t)p.M;
+  const uint32_t m = pair - bq * (uint32_t)p.M;
   const uint32_t l = fdiv(s, p.div_k);
   const uint64_t pi = (uint64_t)pair * (uint32_t)p.LK + s;
-  float locx, locy;
-  load_xy<T>(p.loc, pi, locx, locy);
-  const float a = load1<T>(p.attn, pi);
   const int32_t H = lt.h[l], W = lt.w[l], st = lt.start[l];
   const float fw = (float)W, fh = (float)H;
-  const float x = __fsub_rn(__fmul_rn(locx, fw), 0.5f);
-  const float y = __fsub_rn(__fmul_rn(locy, fh), 0.5f);
+  float x, y, a;
+  if constexpr (FUSED) {
+    float rx, ry, ox, oy;
+    load_xy<T>(p.ref, p.ref_levels ? (uint64_t)bq * (uint32_t)p.L + l : (uint64_t)bq, rx, ry);
+    load_xy<T>(p.loc, pi, ox, oy);
+    x = __fsub_rn(__fmaf_rn(rx, fw, ox), 0.5f);
+    y = __fsub_rn(__fmaf_rn(ry, fh, oy), 0.5f);
+    a = expf(load1<T>(p.attn, pi) - lse);
+  } else {
+    float locx, locy;
+    load_xy<T>(p.loc, pi, locx, locy);
+    a = load1<T>(p.attn, pi);
+    x = __fsub_rn(__fmul_rn(locx, fw), 0.5f);
+    y = __fsub_rn(__fmul_rn(locy, fh), 0.5f);
+  }
   float x0f = floorf(x), y0f = floorf(y);
   r.lx = x - x0f;
   r.ly = y - y0f;

@@ -17,6 +17,12 @@
 //     flight (4 corner loads each);
 //   * the TS partial sums are folded with DPP / permlane exchanges and slot 0
 //     stores its CB bytes of the output row.
+//
+// FUSED = true is the fused MSDeformAttn front-end (labs/solutions/lab00.py:
+// 194-208): the staging turns reference points, per-level pixel offsets and
+// attention logits into locations and softmax weights, after a prologue that
+// computes each pair's log-sum-exp (kept in LDS and, for the backward, in
+// p.lse).  The (B,Q,M,L,K) locations and weights never exist in memory.
 #include "msda_launch.h"
 
 namespace msda {
@@ -25,7 +31,7 @@ namespace {
 
 constexpr int kUnroll = 4;
 
-template <class T, int CB, int G, int TS>
+template <class T, int CB, int G, int TS, bool FUSED>
 __global__ __launch_bounds__(kBlock) void fwd_kernel(Params p) {
   using C = Chunk<T, CB>;
   constexpr int kVec = C::kVec;
@@ -35,6 +41,7 @@ __global__ __launch_bounds__(kBlock) void fwd_kernel(Params p) {
   __shared__ LevelTable lt;
   __shared__ uint4 s_off[kMaxRecords];
   __shared__ float4 s_w[kMaxRecords];
+  __shared__ float s_lse[FUSED ? kBlock : 1];
 
   const int g = kStatic ? G : p.g_rt;
   const int ts = kStatic ? TS : p.ts_rt;
@@ -54,6 +61,7 @@ __global__ __launch_bounds__(kBlock) void fwd_kernel(Params p) {
   const uint32_t chb = live ? (uint32_t)(ch * CB) : kDeadLaneBytes;
 
   load_levels(p, lt);
+  if constexpr (FUSED) pair_lse<T>(p, pair0, ppb, team, s_lse);
   __syncthreads();
 
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value, p.value_bytes);
@@ -70,8 +78,9 @@ __global__ __launch_bounds__(kBlock) void fwd_kernel(Params p) {
       const int jp = j >> p.log2_sch;
       const int s = pass * p.sch + (j & (p.sch - 1));
       const int pr = pair0 + jp;
-      const Sample q = make_sample<T>(p, lt, (uint32_t)pr, (uint32_t)s,
-                                      pr < p.npairs && s < p.LK);
+      const Sample q = make_sample<T, FUSED>(p, lt, (uint32_t)pr, (uint32_t)s,
+                                             pr < p.npairs && s < p.LK,
+                                             FUSED ? s_lse[jp] : 0.f);
       const float w1x = 1.f - q.lx, w1y = 1.f - q.ly;
       s_off[j] = make_uint4(q.off[0] * T::kBytes, q.off[1] * T::kBytes, q.off[2] * T::kBytes,
                             q.off[3] * T::kBytes);
@@ -128,45 +137,51 @@ __global__ __launch_bounds__(kBlock) void fwd_kernel(Params p) {
   }
 }
 
-template <class T, int CB, int G, int TS>
+template <class T, int CB, int G, int TS, bool FUSED>
 hipError_t launch_one(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((fwd_kernel<T, CB, G, TS>), dim3(p.nblocks), dim3(kBlock), 0, st, p);
+  hipLaunchKernelGGL((fwd_kernel<T, CB, G, TS, FUSED>), dim3(p.nblocks), dim3(kBlock), 0, st, p);
   return hipGetLastError();
 }
 
-template <class T>
+template <class T, bool FUSED>
 hipError_t dispatch(const Shape& s, const Params& p, hipStream_t st) {
   switch (s.cb * 10000 + s.g * 100 + s.ts) {
-    case 160201: return launch_one<T, 16, 2, 1>(p, st);
-    case 160204: return launch_one<T, 16, 2, 4>(p, st);
-    case 160216: return launch_one<T, 16, 2, 16>(p, st);
-    case 160401: return launch_one<T, 16, 4, 1>(p, st);
-    case 160404: return launch_one<T, 16, 4, 4>(p, st);
-    case 160416: return launch_one<T, 16, 4, 16>(p, st);
-    case 160801: return launch_one<T, 16, 8, 1>(p, st);
-    case 160804: return launch_one<T, 16, 8, 4>(p, st);
-    case 161601: return launch_one<T, 16, 16, 1>(p, st);
-    case 161604: return launch_one<T, 16, 16, 4>(p, st);
+    case 160201: return launch_one<T, 16, 2, 1, FUSED>(p, st);
+    case 160204: return launch_one<T, 16, 2, 4, FUSED>(p, st);
+    case 160216: return launch_one<T, 16, 2, 16, FUSED>(p, st);
+    case 160401: return launch_one<T, 16, 4, 1, FUSED>(p, st);
+    case 160404: return launch_one<T, 16, 4, 4, FUSED>(p, st);
+    case 160416: return launch_one<T, 16, 4, 16, FUSED>(p, st);
+    case 160801: return launch_one<T, 16, 8, 1, FUSED>(p, st);
+    case 160804: return launch_one<T, 16, 8, 4, FUSED>(p, st);
+    case 161601: return launch_one<T, 16, 16, 1, FUSED>(p, st);
+    case 161604: return launch_one<T, 16, 16, 4, FUSED>(p, st);
     default: break;
   }
-  if (s.cb == 16) return launch_one<T, 16, 0, 0>(p, st);
-  if (s.cb == 8) return launch_one<T, 8, 0, 0>(p, st);
-  if (s.cb == 4) return launch_one<T, 4, 0, 0>(p, st);
+  if (s.cb == 16) return launch_one<T, 16, 0, 0, FUSED>(p, st);
+  if (s.cb == 8) return launch_one<T, 8, 0, 0, FUSED>(p, st);
+  if (s.cb == 4) return launch_one<T, 4, 0, 0, FUSED>(p, st);
   if constexpr (T::kBytes == 2) {
-    if (s.cb == 2) return launch_one<T, 2, 0, 0>(p, st);
+    if (s.cb == 2) return launch_one<T, 2, 0, 0, FUSED>(p, st);
   }
   return hipErrorInvalidValue;
 }
 
-}  // namespace
-
-hipError_t launch_forward(int dtype, const Shape& s, const Params& p, hipStream_t st) {
+template <bool FUSED>
+hipError_t dispatch_dtype(int dtype, const Shape& s, const Params& p, hipStream_t st) {
   switch (dtype) {
-    case kF32: return dispatch<F32>(s, p, st);
-    case kF16: return dispatch<F16>(s, p, st);
-    case kBF16: return dispatch<BF16>(s, p, st);
+    case kF32: return dispatch<F32, FUSED>(s, p, st);
+    case kF16: return dispatch<F16, FUSED>(s, p, st);
+    case kBF16: return dispatch<BF16, FUSED>(s, p, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+}  // namespace
+
+hipError_t launch_forward(int dtype, bool fused, const Shape& s, const Params& p,
+                          hipStream_t st) {
+  return fused ? dispatch_dtype<true>(dtype, s, p, st) : dispatch_dtype<false>(dtype, s, p, st);
 }
 
 }  // namespace msda

@@ -30,14 +30,20 @@ bool choose_shape(int row_bytes, int lk, int64_t npairs, bool backward, int ts_p
 // for a kernel that stages at most `max_records` samples per pass.
 void finish_params(const Shape& s, int max_records, Params* p);
 
-hipError_t launch_forward(int dtype, const Shape& s, const Params& p, hipStream_t st);
-hipError_t launch_backward(int dtype, bool fp32_acc, const Shape& s, const Params& p,
-                           hipStream_t st);
-// LDS-privatised backward (msda_backward_priv.hip).
+// `fused`: the fused front-end variants (offsets + logits instead of
+// locations + weights; see Params).
+hipError_t launch_forward(int dtype, bool fused, const Shape& s, const Params& p,
+                          hipStream_t st);
+hipError_t launch_backward(int dtype, bool fp32_acc, bool fused, const Shape& s,
+                           const Params& p, hipStream_t st);
+// Row-dedup backward (msda_backward_priv.hip).
 bool priv_supported(const Shape& s, int D, int K, int elem_bytes);
 void priv_params(Params* p);
-hipError_t launch_backward_priv(int dtype, bool fp32_acc, const Shape& s, const Params& p,
-                                hipStream_t st);
+hipError_t launch_backward_priv(int dtype, bool fp32_acc, bool fused, const Shape& s,
+                                const Params& p, hipStream_t st);
+// Fused front-end: reference-point gradient from the offset gradients, one
+// wave per (b, q) of the nbq in the call.
+hipError_t launch_ref_grad(int dtype, const Params& p, uint64_t nbq, hipStream_t st);
 hipError_t launch_zero(void* ptr, uint64_t bytes, hipStream_t st);
 hipError_t launch_cast(int dtype, const float* src, void* dst, uint64_t n, hipStream_t st);
 

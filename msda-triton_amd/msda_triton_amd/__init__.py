@@ -8,12 +8,13 @@ kernels for gfx950 (libmsda_hip.so).
 from .ops import multi_scale_deformable_attention
 
 __all__ = ["multi_scale_deformable_attention", "msda_op", "MultiScaleDeformableAttnFunction",
-           "MSDeformAttnFunction"]
+           "MSDeformAttnFunction", "multi_scale_deformable_attention_fused", "MSDACrossAttention"]
 
 
 def __getattr__(name):
-    # torch.library registration and the mmcv / Deformable-DETR shims load on
-    # first use, keeping `import msda_triton_amd` as light as the reference's.
+    # torch.library registration, the mmcv / Deformable-DETR shims and the
+    # fused front-end load on first use, keeping `import msda_triton_amd` as
+    # light as the reference's.
     if name == "msda_op":
         from .library import msda_op
 
@@ -22,6 +23,10 @@ def __getattr__(name):
         from . import compat
 
         return getattr(compat, name)
+    if name in ("multi_scale_deformable_attention_fused", "MSDACrossAttention"):
+        from . import fused
+
+        return getattr(fused, name)
     raise AttributeError(name)
 
 

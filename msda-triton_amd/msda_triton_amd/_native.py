@@ -30,6 +30,8 @@ _INT = ctypes.c_int
 SIGNATURES = {
     "msda_forward": (_INT, [_P, _P, _P, _P, _P, _P] + [_I64] * 7 + [_INT, _P]),
     "msda_backward": (_INT, [_P] * 10 + [_I64] * 7 + [_INT, _P]),
+    "msda_fused_forward": (_INT, [_P] * 8 + [_I64] * 7 + [_INT, _INT, _P]),
+    "msda_fused_backward": (_INT, [_P] * 14 + [_I64] * 7 + [_INT, _INT, _P]),
     "msda_error_string": (ctypes.c_char_p, [_INT]),
     "msda_abi_version": (_INT, []),
 }

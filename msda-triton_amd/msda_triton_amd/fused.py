@@ -1,0 +1,243 @@
+"""Fused MSDeformAttn front-end: softmax of the attention logits and
+reference point + offset / (W_l, H_l) computed inside the HIP kernels.
+
+The reference's attention layer (labs/solutions/lab00.py:194-208,
+``MSDACrossAttention.forward``) builds the operator's inputs with three
+PyTorch ops
+
+    weights   = weight_proj(query).reshape(B, Q, M, L*K).softmax(-1)
+    locations = reference_points[:, :, None, None, None, :]
+                + offsets / spatial_shapes.flip(-1)[None, None, None, :, None, :]
+
+and then calls ``multi_scale_deformable_attention``.  Here the kernels take
+the reference points, offsets and logits directly (C ABI
+``msda_fused_forward`` / ``msda_fused_backward``), so the (B, Q, M, L, K)
+locations and weights are never written to or read back from memory, and
+their backward (softmax backward, division, broadcast sum) happens in the
+same kernels.  The forward also returns each (b, q, m)'s log-sum-exp of the
+logits, which the backward reuses.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+from torch.autograd.function import once_differentiable
+
+from . import _native
+from .ops import _DTYPE_CODE, _FLOAT_DTYPES, _use_fp32_grad_accum
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def fused_forward_raw(value, spatial_shapes, level_start_index, reference_points,
+                      sampling_offsets, attention_logits, ref_levels: int, need_lse: bool = True):
+    """One call of ``msda_fused_forward`` on prepared (contiguous, validated)
+    tensors.  Returns ``(out (B, Q, M, D), lse (B, Q, M) fp32 or None)``."""
+    B, S, M, D = value.shape
+    _, Q, _, L, K, _ = sampling_offsets.shape
+    out = value.new_empty(B, Q, M, D)
+    lse = (torch.empty(B, Q, M, dtype=torch.float32, device=value.device)
+           if need_lse else None)
+    lib = _native.load()
+    with torch.cuda.device(value.device):
+        rc = lib.msda_fused_forward(
+            _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(reference_points),
+            _ptr(sampling_offsets), _ptr(attention_logits), _ptr(out), _ptr(lse),
+            B, S, M, D, Q, L, K, ref_levels, _DTYPE_CODE[value.dtype], _stream(value))
+    _native.check(rc, "msda_fused_forward")
+    return out, lse
+
+
+def fused_backward_raw(value, spatial_shapes, level_start_index, reference_points,
+                       sampling_offsets, attention_logits, lse, out, grad_out, ref_levels: int,
+                       fp32_grad_accum: bool, need_ref_grad: bool = True):
+    """One call of ``msda_fused_backward``.  Returns ``(grad_value,
+    grad_reference_points or None, grad_offsets, grad_logits)``."""
+    B, S, M, D = value.shape
+    _, Q, _, L, K, _ = sampling_offsets.shape
+    grad_out = grad_out.reshape(B, Q, M, D).contiguous()
+    grad_value = torch.empty_like(value)  # zero-filled by the library
+    accum = None
+    if fp32_grad_accum and value.dtype != torch.float32:
+        accum = torch.empty(value.shape, dtype=torch.float32, device=value.device)
+    grad_ref = torch.empty_like(reference_points) if need_ref_grad else None
+    grad_off = torch.empty_like(sampling_offsets)
+    grad_logits = torch.empty_like(attention_logits)
+    lib = _native.load()
+    with torch.cuda.device(value.device):
+        rc = lib.msda_fused_backward(
+            _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(reference_points),
+            _ptr(sampling_offsets), _ptr(attention_logits), _ptr(lse), _ptr(out),
+            _ptr(grad_out), _ptr(grad_value), _ptr(accum), _ptr(grad_ref), _ptr(grad_off),
+            _ptr(grad_logits), B, S, M, D, Q, L, K, ref_levels, _DTYPE_CODE[value.dtype],
+            _stream(value))
+    _native.check(rc, "msda_fused_backward")
+    return grad_value, grad_ref, grad_off, grad_logits
+
+
+class _FusedMSDAFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, value, spatial_shapes, level_start_index, reference_points,
+                sampling_offsets, attention_logits, fp32_grad_accum, ref_levels):
+        out, lse = fused_forward_raw(value, spatial_shapes, level_start_index, reference_points,
+                                     sampling_offsets, attention_logits, ref_levels)
+        ctx.save_for_backward(value, spatial_shapes, level_start_index, reference_points,
+                              sampling_offsets, attention_logits, lse, out)
+        ctx.fp32_grad_accum = fp32_grad_accum
+        ctx.ref_levels = ref_levels
+        B, Q, M, D = out.shape
+        return out.view(B, Q, M * D)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_out):
+        (value, spatial_shapes, level_start_index, reference_points, sampling_offsets,
+         attention_logits, lse, out) = ctx.saved_tensors
+        gv, gref, goff, glog = fused_backward_raw(
+            value, spatial_shapes, level_start_index, reference_points, sampling_offsets,
+            attention_logits, lse, out, grad_out, ctx.ref_levels, ctx.fp32_grad_accum,
+            need_ref_grad=ctx.needs_input_grad[3])
+        return gv, None, None, gref, goff, glog, None, None
+
+
+def _prepare_fused(value, spatial_shapes, level_start_index, reference_points, sampling_offsets,
+                   attention_logits, fp32_grad_accum):
+    """Validation and defaults.  Returns the empty output for B == 0 or Q == 0,
+    else the argument tuple of the device computation (logits viewed as
+    (B, Q, M, L, K))."""
+    if value.dim() != 4:
+        raise ValueError(f"value must be (B, S, M, D), got {tuple(value.shape)}")
+    if sampling_offsets.dim() != 6 or sampling_offsets.shape[-1] != 2:
+        raise ValueError(
+            f"sampling_offsets must be (B, Q, M, L, K, 2), got {tuple(sampling_offsets.shape)}")
+    B, S, M, D = value.shape
+    _, Q, _, L, K, _ = sampling_offsets.shape
+    if sampling_offsets.shape[0] != B or sampling_offsets.shape[2] != M:
+        raise ValueError(f"sampling_offsets {tuple(sampling_offsets.shape)} inconsistent with "
+                         f"value {tuple(value.shape)}")
+    if attention_logits.shape == (B, Q, M, L * K):
+        attention_logits = attention_logits.reshape(B, Q, M, L, K)
+    if attention_logits.shape != (B, Q, M, L, K):
+        raise ValueError(f"attention_logits must be {(B, Q, M, L, K)} or {(B, Q, M, L * K)}, "
+                         f"got {tuple(attention_logits.shape)}")
+    if reference_points.shape == (B, Q, 2):
+        ref_levels = 0
+    elif reference_points.shape == (B, Q, L, 2):
+        ref_levels = 1
+    else:
+        raise ValueError(f"reference_points must be {(B, Q, 2)} or {(B, Q, L, 2)}, got "
+                         f"{tuple(reference_points.shape)}")
+    if spatial_shapes.shape != (L, 2):
+        raise ValueError(f"spatial_shapes must be ({L}, 2), got {tuple(spatial_shapes.shape)}")
+    dtypes = {value.dtype, sampling_offsets.dtype, attention_logits.dtype, reference_points.dtype}
+    if len(dtypes) != 1:
+        raise ValueError(
+            f"value/reference_points/sampling_offsets/attention_logits dtypes must match, got "
+            f"{value.dtype}/{reference_points.dtype}/{sampling_offsets.dtype}/"
+            f"{attention_logits.dtype}")
+    if value.dtype not in _FLOAT_DTYPES:
+        raise ValueError(f"unsupported dtype {value.dtype}; use fp32, fp16 or bf16")
+    if value.device.type != "cuda":
+        raise ValueError("the operator requires CUDA-API (ROCm/HIP) device tensors")
+    devices = {value.device, reference_points.device, sampling_offsets.device,
+               attention_logits.device}
+    if len(devices) != 1:
+        raise ValueError("value, reference_points, sampling_offsets and attention_logits must "
+                         "share a device")
+
+    spatial_shapes = spatial_shapes.to(device=value.device, dtype=torch.int64).contiguous()
+    if level_start_index is None:
+        hw = spatial_shapes.prod(-1)
+        level_start_index = torch.cat([hw.new_zeros(1), hw.cumsum(0)[:-1]])
+    else:
+        if level_start_index.shape != (L,):
+            raise ValueError(
+                f"level_start_index must be ({L},), got {tuple(level_start_index.shape)}")
+        level_start_index = level_start_index.to(device=value.device, dtype=torch.int64).contiguous()
+
+    if B == 0 or Q == 0:
+        return value.new_zeros(B, Q, M * D)
+    if fp32_grad_accum is None:
+        fp32_grad_accum = _use_fp32_grad_accum(value)
+    return (value.contiguous(), spatial_shapes, level_start_index, reference_points.contiguous(),
+            sampling_offsets.contiguous(), attention_logits.contiguous(), bool(fp32_grad_accum),
+            ref_levels)
+
+
+def multi_scale_deformable_attention_fused(
+    value: torch.Tensor,
+    spatial_shapes: torch.Tensor,
+    level_start_index: torch.Tensor | None,
+    reference_points: torch.Tensor,
+    sampling_offsets: torch.Tensor,
+    attention_logits: torch.Tensor,
+    *,
+    fp32_grad_accum: bool | None = None,
+) -> torch.Tensor:
+    """``multi_scale_deformable_attention(value, spatial_shapes,
+    level_start_index, ref + offsets / (W_l, H_l), softmax(logits))`` in one
+    fused operator (math of labs/solutions/lab00.py:201-208).
+
+    Args:
+        value: ``(B, S, M, D)``.
+        spatial_shapes: ``(L, 2)`` integer ``(H_l, W_l)``.
+        level_start_index: ``(L,)`` or ``None``.
+        reference_points: ``(B, Q, 2)`` (shared by all levels) or
+            ``(B, Q, L, 2)`` (per level), normalised ``(x, y)``.
+        sampling_offsets: ``(B, Q, M, L, K, 2)`` in level-l pixel units.
+        attention_logits: ``(B, Q, M, L, K)`` or ``(B, Q, M, L*K)``; the
+            softmax runs over the L*K points of each (b, q, m).
+        fp32_grad_accum: as in ``multi_scale_deformable_attention``.
+
+    Returns:
+        ``(B, Q, M * D)`` in the value dtype.  Differentiable in value,
+        reference_points, sampling_offsets and attention_logits.
+    """
+    prep = _prepare_fused(value, spatial_shapes, level_start_index, reference_points,
+                          sampling_offsets, attention_logits, fp32_grad_accum)
+    if isinstance(prep, torch.Tensor):
+        return prep
+    return _FusedMSDAFunction.apply(*prep)
+
+
+class MSDACrossAttention(nn.Module):
+    """Deformable-DETR style multi-scale deformable attention layer on the
+    fused operator.  Same constructor, parameters and forward contract as the
+    reference's layer (labs/solutions/lab00.py:169-208): value/offset/weight/
+    output projections; offsets in each level's pixel units; softmax over all
+    L*K points; ``reference_points`` ``(B, Q, 2)`` (or ``(B, Q, L, 2)``) in
+    [0, 1].  Returns ``(B, Q, C)``."""
+
+    def __init__(self, embed_dim: int, num_heads: int, num_levels: int, num_points: int):
+        super().__init__()
+        if embed_dim % num_heads != 0:
+            raise ValueError("embed_dim must be divisible by num_heads")
+        self.num_heads = num_heads
+        self.num_levels = num_levels
+        self.num_points = num_points
+        self.head_dim = embed_dim // num_heads
+        M, L, K = num_heads, num_levels, num_points
+        self.value_proj = nn.Linear(embed_dim, embed_dim)
+        self.offset_proj = nn.Linear(embed_dim, M * L * K * 2)
+        self.weight_proj = nn.Linear(embed_dim, M * L * K)
+        self.out_proj = nn.Linear(embed_dim, embed_dim)
+
+    def forward(self, query, reference_points, value, spatial_shapes, level_start_index=None,
+                *, fp32_grad_accum=None):
+        B, Q, _ = query.shape
+        _, S, _ = value.shape
+        M, L, K, D = self.num_heads, self.num_levels, self.num_points, self.head_dim
+        v = self.value_proj(value).reshape(B, S, M, D)
+        offsets = self.offset_proj(query).reshape(B, Q, M, L, K, 2)
+        logits = self.weight_proj(query).reshape(B, Q, M, L, K)
+        out = multi_scale_deformable_attention_fused(
+            v, spatial_shapes, level_start_index, reference_points, offsets, logits,
+            fp32_grad_accum=fp32_grad_accum)
+        return self.out_proj(out)

@@ -11,6 +11,8 @@ roulbac/msda-triton:
   msda_naive              float64 loops                tests/reference_impls.py:48-87
   msda_backward_analytic  flat-index hand gradients    labs/solutions/lab07.py:12-104
   run_reference(_fp32)    CPU upcast protocol          tests/test_msda.py:80-93
+  msda_fused_reference    front-end + operator         labs/solutions/lab00.py:201-208
+  run_fused_reference     its CPU upcast protocol (fwd + 4 gradients)
 Every function is pinned by tests/test_oracle.py (naive vs grid_sample in
 float64, closed forms, gradcheck, adjoint identity, planted-mistake checks).
 """
@@ -18,8 +20,10 @@ float64, closed forms, gradcheck, adjoint identity, planted-mistake checks).
 from .msda_reference import (  # noqa: F401
     level_start_index_of,
     msda_backward_analytic,
+    msda_fused_reference,
     msda_naive,
     msda_reference,
+    run_fused_reference,
     run_reference,
     run_reference_fp32,
 )

@@ -195,3 +195,40 @@ def run_reference(value, spatial_shapes, loc, attn, grad_out=None, dtype=torch.f
 def run_reference_fp32(value, spatial_shapes, loc, attn, grad_out=None):
     """The reference's fp32 CPU protocol (tests/test_msda.py:80-93)."""
     return run_reference(value, spatial_shapes, loc, attn, grad_out, dtype=torch.float32)
+
+
+def msda_fused_reference(value, spatial_shapes, reference_points, sampling_offsets,
+                         attention_logits):
+    """The attention layer's front-end composed with the operator, as the
+    reference's MSDACrossAttention.forward does it (labs/solutions/lab00.py:
+    201-208): softmax of the logits over the L*K points of each (b, q, m),
+    locations = reference point + offset / (W_l, H_l), then
+    ``msda_reference``.  ``reference_points`` is (B, Q, 2) as there, or
+    (B, Q, L, 2) (one point per level, the Deformable-DETR layout).
+    Differentiable in all four tensors through torch autograd."""
+    B, Q, M, L, K, _ = sampling_offsets.shape
+    weights = attention_logits.reshape(B, Q, M, L * K).softmax(-1).reshape(B, Q, M, L, K)
+    scale = spatial_shapes.flip(-1).to(sampling_offsets.dtype)  # (L, 2) as (W_l, H_l)
+    if reference_points.dim() == 3:
+        ref = reference_points[:, :, None, None, None, :]
+    else:
+        ref = reference_points[:, :, None, :, None, :]
+    locs = ref + sampling_offsets / scale[None, None, None, :, None, :]
+    return msda_reference(value, spatial_shapes, locs, weights)
+
+
+def run_fused_reference(value, spatial_shapes, reference_points, sampling_offsets,
+                        attention_logits, grad_out=None, dtype=torch.float64):
+    """``msda_fused_reference`` on CPU leaf copies upcast to `dtype`, with the
+    four gradients when grad_out is given.  Returns (out, grads or None), grads
+    ordered (value, reference_points, sampling_offsets, attention_logits)."""
+    shapes = spatial_shapes.cpu()
+    grad = grad_out is not None
+    leaves = [t.detach().to(dtype).cpu().requires_grad_(grad)
+              for t in (value, reference_points, sampling_offsets, attention_logits)]
+    if not grad:
+        with torch.no_grad():
+            return msda_fused_reference(leaves[0], shapes, *leaves[1:]), None
+    out = msda_fused_reference(leaves[0], shapes, *leaves[1:])
+    out.backward(grad_out.detach().to(dtype).cpu())
+    return out.detach(), tuple(t.grad for t in leaves)

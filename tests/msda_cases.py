@@ -60,3 +60,45 @@ def rel_err(x: torch.Tensor, ref: torch.Tensor) -> float:
     den = ref.norm().item()
     num = (x - ref).norm().item()
     return num / den if den > 0 else num
+
+
+def make_fused_inputs(B, Q, M, D, shapes, K, dtype, device, per_level=False, offset_sigma=2.0,
+                      logit_sigma=1.0, seed=0):
+    """Inputs of the fused front-end: value N(0,1); reference points U[0,1)
+    ((B,Q,2), or (B,Q,L,2) when per_level); offsets N(0, offset_sigma) in
+    level pixels (so points near a border fall outside); logits
+    N(0, logit_sigma).  Drawn on a CPU generator, then cast and moved."""
+    gen = torch.Generator().manual_seed(seed)
+    L = len(shapes)
+    S = sum(h * w for h, w in shapes)
+    value = torch.randn(B, S, M, D, generator=gen)
+    ref = torch.rand(*((B, Q, L, 2) if per_level else (B, Q, 2)), generator=gen)
+    off = offset_sigma * torch.randn(B, Q, M, L, K, 2, generator=gen)
+    logits = logit_sigma * torch.randn(B, Q, M, L, K, generator=gen)
+    ref = ref.to(dtype)
+    off = _off_knots(off.to(dtype), ref, shapes, per_level)
+    spatial_shapes = torch.tensor(shapes, dtype=torch.long, device=device)
+    hw = spatial_shapes.prod(-1)
+    starts = torch.cat([hw.new_zeros(1), hw.cumsum(0)[:-1]])
+    cast = lambda t: t.to(device, dtype)  # noqa: E731
+    return cast(value), spatial_shapes, starts, cast(ref), cast(off), cast(logits)
+
+
+def _off_knots(off, ref, shapes, per_level, margin=1e-3):
+    """Nudge (in the storage dtype) every offset whose image coordinate
+    ref * W + offset - 0.5 lies within `margin` px of an integer.  At such a
+    bilinear knot d(out)/d(location) jumps, and which side an implementation
+    lands on depends on its last rounding (the float64 oracle's included), so
+    gradients there are not comparable.  Half-precision inputs hit knots
+    exactly with noticeable probability."""
+    dtype = off.dtype
+    sizes = torch.tensor([[w, h] for h, w in shapes], dtype=torch.float64)  # (L, 2) as (W, H)
+    r = ref.double()[:, :, None, :, None, :] if per_level else ref.double()[:, :, None, None, None, :]
+    for step in (0.05, 0.1, 0.2, 0.4):
+        o = off.double()
+        x = r * sizes[None, None, None, :, None, :] + o - 0.5
+        near = (x - x.round()).abs() < margin
+        if not near.any():
+            break
+        off = torch.where(near, (o + step).to(dtype), off)
+    return off
