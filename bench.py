@@ -21,6 +21,9 @@ Prints ONE JSON line:
   roofline_fwd forward kernel vs 8 TB/s HBM (the operator's stated target)
   other_presets fwd / bwd / fwd+bwd device times and GB/s of the other
                benchmark presets (encoder, high-contention, Mask2Former, tiny)
+  fused_front_end  decoder shapes: the fused MSDeformAttn front-end (softmax,
+               reference point + offset in the kernels) vs the same front-end
+               composed from PyTorch ops around the operator
   cpu_baseline the CPU oracle (grid_sample restatement) on the host cores
 """
 
@@ -102,10 +105,46 @@ def cpu_baseline(preset: str, max_seconds: float = 25.0) -> dict:
     }
 
 
-def preset_device_times(preset: str, lib, fp32_grad_accum: bool = False, reps: int = 10,
-                        replays: int = 5) -> dict:
-    """fwd / bwd / fwd+bwd device time of one preset: HIP events around
-    replays of a HIP graph holding `reps` back-to-back C-ABI calls."""
+def _capture(fn, reps, dev):
+    """A HIP graph of `reps` back-to-back calls of fn (warmed up on a side
+    stream first, as graph capture requires)."""
+    import torch
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def _graph_us(fn, dev, reps=10, replays=5):
+    """Device time per call: HIP events on the launch stream around
+    `replays` replays of a graph holding `reps` calls."""
+    import torch
+
+    graph = _capture(fn, reps, dev)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * replays)
+
+
+def preset_device_times(preset: str, lib, fp32_grad_accum: bool = False) -> dict:
+    """fwd / bwd / fwd+bwd device time of one preset (graph-replayed C-ABI
+    calls, see _graph_us)."""
     import torch
 
     from msda_triton_amd import _native, presets
@@ -135,34 +174,81 @@ def preset_device_times(preset: str, lib, fp32_grad_accum: bool = False, reps: i
                                         gl.data_ptr(), ga.data_ptr(), *dims, dt,
                                         torch.cuda.current_stream().cuda_stream), "msda_backward")
 
-    def timed(fn):
-        side = torch.cuda.Stream(device=dev)
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            for _ in range(2):
-                fn()
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for _ in range(reps):
-                fn()
-        graph.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(replays):
-            graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (reps * replays)
-
-    f_us, b_us = timed(fwd), timed(bwd)
+    f_us, b_us = _graph_us(fwd, dev), _graph_us(bwd, dev)
     fb, bb = presets.algorithmic_bytes(preset)
     return {"fwd_us": round(f_us, 2), "bwd_us": round(b_us, 2), "fwd_bwd_us": round(f_us + b_us, 2),
             "fwd_gbps": round(fb / f_us / 1e3, 1), "bwd_gbps": round(bb / b_us / 1e3, 1),
             "fwd_bwd_gbps": round((fb + bb) / (f_us + b_us) / 1e3, 1),
             "grad_value_accum": "fp32" if accum is not None else str(value.dtype).split(".")[-1]}
+
+
+def fused_front_end_times(lib, preset: str = "decoder") -> dict:
+    """The fused MSDeformAttn front-end (msda_fused_forward / _backward,
+    per-level reference points) against the same front-end composed from
+    PyTorch ops around the plain operator, as the reference's attention layer
+    does it (labs/solutions/lab00.py:201-208; backward: softmax backward,
+    offset division and reference-point sum, as autograd runs them).  Both
+    graph-replayed; device time per call."""
+    import torch
+
+    from msda_triton_amd import _native, presets
+    from msda_triton_amd.ops import _DTYPE_CODE
+
+    dev = torch.device("cuda", 0)
+    c = presets.preset_dims(preset)
+    B, S, M, D, Q, L, K = c["B"], c["S"], c["M"], c["D"], c["Q"], c["L"], c["K"]
+    value, shapes, starts, ref, off, logits = presets.make_fused_preset_inputs(preset, dev)
+    grad_out = presets.make_grad_out(preset, device=dev)
+    dt = _DTYPE_CODE[value.dtype]
+    dims = (B, S, M, D, Q, L, K)
+    out = torch.empty(B, Q, M, D, dtype=value.dtype, device=dev)
+    lse = torch.empty(B, Q, M, dtype=torch.float32, device=dev)
+    gv, gref = torch.empty_like(value), torch.empty_like(ref)
+    goff, glog = torch.empty_like(off), torch.empty_like(logits)
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def fused_fwd():
+        _native.check(lib.msda_fused_forward(
+            value.data_ptr(), shapes.data_ptr(), starts.data_ptr(), ref.data_ptr(),
+            off.data_ptr(), logits.data_ptr(), out.data_ptr(), lse.data_ptr(), *dims, 1, dt,
+            st()), "msda_fused_forward")
+
+    def fused_bwd():
+        _native.check(lib.msda_fused_backward(
+            value.data_ptr(), shapes.data_ptr(), starts.data_ptr(), ref.data_ptr(),
+            off.data_ptr(), logits.data_ptr(), lse.data_ptr(), out.data_ptr(),
+            grad_out.data_ptr(), gv.data_ptr(), None, gref.data_ptr(), goff.data_ptr(),
+            glog.data_ptr(), *dims, 1, dt, st()), "msda_fused_backward")
+
+    scale = shapes.flip(-1).to(value.dtype)[None, None, None, :, None, :]
+    loc = ref[:, :, None, :, None, :] + off / scale
+    attn = logits.reshape(B, Q, M, L * K).softmax(-1)
+    gloc, gattn = torch.empty_like(off), torch.empty(B, Q, M, L * K, dtype=value.dtype,
+                                                        device=dev)
+
+    def composed_fwd():
+        lo = ref[:, :, None, :, None, :] + off / scale
+        at = logits.reshape(B, Q, M, L * K).softmax(-1)
+        _native.check(lib.msda_forward(value.data_ptr(), shapes.data_ptr(), starts.data_ptr(),
+                                       lo.data_ptr(), at.data_ptr(), out.data_ptr(), *dims, dt,
+                                       st()), "msda_forward")
+
+    def composed_bwd():
+        _native.check(lib.msda_backward(value.data_ptr(), shapes.data_ptr(), starts.data_ptr(),
+                                        loc.data_ptr(), attn.data_ptr(), grad_out.data_ptr(),
+                                        gv.data_ptr(), None, gloc.data_ptr(), gattn.data_ptr(),
+                                        *dims, dt, st()), "msda_backward")
+        torch._softmax_backward_data(gattn, attn, -1, value.dtype)
+        torch.div(gloc, scale)
+        gloc.sum((2, 4))
+
+    res = {"preset": preset, "reference_points": "(B, Q, L, 2)",
+           "fused_fwd_us": _graph_us(fused_fwd, dev), "fused_bwd_us": _graph_us(fused_bwd, dev),
+           "composed_fwd_us": _graph_us(composed_fwd, dev),
+           "composed_bwd_us": _graph_us(composed_bwd, dev)}
+    res["fused_fwd_bwd_us"] = res["fused_fwd_us"] + res["fused_bwd_us"]
+    res["composed_fwd_bwd_us"] = res["composed_fwd_us"] + res["composed_bwd_us"]
+    return {k: (round(v, 2) if isinstance(v, float) else v) for k, v in res.items()}
 
 
 OTHER_PRESETS = ("tiny", "encoder", "high_contention", "mask2former_fp32", "mask2former_bf16")
@@ -178,7 +264,7 @@ def main() -> int:
                     help="accumulate grad_value in an fp32 scratch buffer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-presets", action="store_true",
-                    help="skip the device timings of the other presets")
+                    help="skip the other presets and the fused front-end timings")
     ap.add_argument("--pmc-driver", action="store_true",
                     help="for rocprofv3 --pmc runs: a few eager fwd/bwd calls plus a 256 MiB "
                          "device copy (counter calibration); prints no JSON")
@@ -249,19 +335,7 @@ def main() -> int:
         return 0
 
     def capture(fn, reps):
-        side = torch.cuda.Stream(device=dev)
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            for _ in range(3):
-                fn()
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for _ in range(reps):
-                fn()
-        torch.cuda.synchronize()
-        return graph
+        return _capture(fn, reps, dev)
 
     step_graph = capture(step, 1)
     for _ in range(args.warmup):
@@ -280,17 +354,7 @@ def main() -> int:
     # Per-call device times: HIP events on the launch stream around replays of
     # graphs holding R back-to-back calls.
     def per_call_us(fn, reps=50, replays=10):
-        graph = capture(fn, reps)
-        graph.replay()
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(replays):
-            graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (reps * replays)
+        return _graph_us(fn, dev, reps, replays)
 
     fwd_us = per_call_us(fwd)
     bwd_us = per_call_us(bwd)
@@ -374,7 +438,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(bwd_gbps / HBM_PEAK_GBPS, 4),
             "traffic": _traffic(args.preset, "backward"),
-            "kernel": "msda_backward call (zero-fill + bwd_kernel)",
+            "kernel": "msda_backward call (zero-fill + row-dedup bwd_priv_kernel)",
             "algorithmic_bytes": bwd_b,
         },
         "roofline_fwd": {
@@ -394,6 +458,7 @@ def main() -> int:
             name: preset_device_times(name, lib)
             for name in OTHER_PRESETS if name != args.preset
         }
+        record["fused_front_end"] = fused_front_end_times(lib)
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline(args.preset)
     print(json.dumps(record), flush=True)

@@ -92,6 +92,27 @@ def make_preset_inputs(name: str, device="cpu", seed: int = 0):
             loc.to(dtype).to(device), attn.to(dtype).to(device))
 
 
+def make_fused_preset_inputs(name: str, device="cpu", seed: int = 0, offset_sigma: float = 2.0):
+    """Inputs of the fused front-end on a preset's shapes: (value,
+    spatial_shapes, level_start_index, reference_points (B, Q, L, 2) ~ U[0, 1),
+    sampling_offsets ~ N(0, offset_sigma) level pixels, attention_logits
+    (B, Q, M, L, K) ~ N(0, 1)); the value tensor is the preset's own draw."""
+    c = preset_dims(name)
+    B, Q, M, D, K, L, S = c["B"], c["Q"], c["M"], c["D"], c["K"], c["L"], c["S"]
+    dtype = c["dtype"]
+    gen = torch.Generator().manual_seed(seed)
+    value = torch.randn(B, S, M, D, generator=gen)
+    ref = torch.rand(B, Q, L, 2, generator=gen)
+    off = offset_sigma * torch.randn(B, Q, M, L, K, 2, generator=gen)
+    logits = torch.randn(B, Q, M, L, K, generator=gen)
+    shapes = torch.tensor(c["shapes"], dtype=torch.int64)
+    hw = shapes.prod(-1)
+    starts = torch.cat([hw.new_zeros(1), hw.cumsum(0)[:-1]])
+    cast = lambda t: t.to(dtype).to(device)  # noqa: E731
+    return (cast(value), shapes.to(device), starts.to(device), cast(ref), cast(off),
+            cast(logits))
+
+
 def make_grad_out(name: str, device="cpu", seed: int = 7) -> torch.Tensor:
     """Seeded N(0, 1) upstream gradient (B, Q, M*D) in the preset dtype."""
     c = preset_dims(name)
