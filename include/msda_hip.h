@@ -159,6 +159,49 @@ int msda_fused_backward(const void* value, const int64_t* spatial_shapes,
                         void* stream);
 
 /*
+ * Deterministic backward.  The reference accumulates grad_value with
+ * floating-point atomics, so its sums depend on their arrival order and are
+ * not reproducible bit for bit (documented at src/msda_triton/ops.py:135-138).
+ * These variants accumulate it in int64 fixed point instead: each
+ * contribution c is added as round(c * 2^e), integer addition is exact, and
+ * the result is identical on every run.  e is chosen per call from
+ * Q*L*K * max|A| * max|grad_output| (a bound on every element) so that no
+ * sum can overflow; the resolution, that bound times 2^-60, is far below
+ * fp32 rounding.  grad_sampling_locations / grad_attention_weights (and the
+ * fused gradients) are deterministic in every variant.
+ *
+ *   workspace   device scratch of msda_deterministic_workspace_bytes(B, S, M,
+ *               D) bytes (the int64 accumulator plus the scale words); its
+ *               contents on entry do not matter.
+ * Other arguments as in msda_backward / msda_fused_backward (no fp32
+ * accumulator: the integer accumulator replaces it).
+ */
+int64_t msda_deterministic_workspace_bytes(int64_t batch, int64_t num_keys, int64_t num_heads,
+                                           int64_t head_dim);
+
+int msda_backward_deterministic(const void* value, const int64_t* spatial_shapes,
+                                const int64_t* level_start_index,
+                                const void* sampling_locations, const void* attention_weights,
+                                const void* grad_output, void* grad_value, void* workspace,
+                                void* grad_sampling_locations, void* grad_attention_weights,
+                                int64_t batch, int64_t num_keys, int64_t num_heads,
+                                int64_t head_dim, int64_t num_queries, int64_t num_levels,
+                                int64_t num_points, int dtype, void* stream);
+
+int msda_fused_backward_deterministic(const void* value, const int64_t* spatial_shapes,
+                                      const int64_t* level_start_index,
+                                      const void* reference_points, const void* sampling_offsets,
+                                      const void* attention_logits, const float* softmax_lse,
+                                      const void* output, const void* grad_output,
+                                      void* grad_value, void* workspace,
+                                      void* grad_reference_points, void* grad_sampling_offsets,
+                                      void* grad_attention_logits, int64_t batch,
+                                      int64_t num_keys, int64_t num_heads, int64_t head_dim,
+                                      int64_t num_queries, int64_t num_levels,
+                                      int64_t num_points, int reference_levels, int dtype,
+                                      void* stream);
+
+/*
  * Human-readable text for a return code (static storage).  The reference has
  * no error channel below Python; this backs the RuntimeError that the host
  * raises for a non-zero code (src/msda_triton/ops.py:165-171 raise the

@@ -80,6 +80,7 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value, p.value_bytes);
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.grad_acc, p.acc_bytes);
   const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.grad_out, p.gout_bytes);
+  const float det_s = A::kBytes == 8 ? det_scale(p) : 0.f;  // int64 fixed-point scale
 
   // grad_out of this lane's pair: its gather chunk (for the dot products)
   // and the words it scatters (zeros for tail pairs and padding lanes).
@@ -173,10 +174,10 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
           // Atomics interleaved with the next samples' gathers measured
           // faster than issuing them all after the gathers (decoder preset).
           if (live) {
-            Sc::add(ra, o[u].x * kAccScale, ch, p.g_real, a * w00, sg);
-            Sc::add(ra, o[u].y * kAccScale, ch, p.g_real, a * w01, sg);
-            Sc::add(ra, o[u].z * kAccScale, ch, p.g_real, a * w10, sg);
-            Sc::add(ra, o[u].w * kAccScale, ch, p.g_real, a * w11, sg);
+            Sc::add(ra, o[u].x * kAccScale, ch, p.g_real, a * w00, sg, det_s);
+            Sc::add(ra, o[u].y * kAccScale, ch, p.g_real, a * w01, sg, det_s);
+            Sc::add(ra, o[u].z * kAccScale, ch, p.g_real, a * w10, sg, det_s);
+            Sc::add(ra, o[u].w * kAccScale, ch, p.g_real, a * w11, sg, det_s);
           }
         }
       }
@@ -227,15 +228,20 @@ hipError_t dispatch(const Shape& s, const Params& p, hipStream_t st) {
 }
 
 template <bool FUSED>
-hipError_t dispatch_dtype(int dtype, bool fp32_acc, const Shape& s, const Params& p,
+hipError_t dispatch_dtype(int dtype, AccMode acc, const Shape& s, const Params& p,
                           hipStream_t st) {
   switch (dtype) {
-    case kF32: return dispatch<F32, F32, FUSED>(s, p, st);
+    case kF32:
+      return acc == kAccI64 ? dispatch<F32, I64, FUSED>(s, p, st)
+                            : dispatch<F32, F32, FUSED>(s, p, st);
     case kF16:
-      return fp32_acc ? dispatch<F16, F32, FUSED>(s, p, st) : dispatch<F16, F16, FUSED>(s, p, st);
+      return acc == kAccI64   ? dispatch<F16, I64, FUSED>(s, p, st)
+             : acc == kAccF32 ? dispatch<F16, F32, FUSED>(s, p, st)
+                              : dispatch<F16, F16, FUSED>(s, p, st);
     case kBF16:
-      return fp32_acc ? dispatch<BF16, F32, FUSED>(s, p, st)
-                      : dispatch<BF16, BF16, FUSED>(s, p, st);
+      return acc == kAccI64   ? dispatch<BF16, I64, FUSED>(s, p, st)
+             : acc == kAccF32 ? dispatch<BF16, F32, FUSED>(s, p, st)
+                              : dispatch<BF16, BF16, FUSED>(s, p, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -313,6 +319,43 @@ __global__ __launch_bounds__(kBlock) void cast_kernel(const float* src, void* ds
   }
 }
 
+// Deterministic backward, before the scatter: max|A| (1 for softmax
+// weights, attn == NULL) and max|grad_out| into det_max[0..1].  For
+// non-negative floats the bit patterns order like the values, so an unsigned
+// integer atomicMax gives the exact maximum whatever the order.
+template <class T>
+__global__ __launch_bounds__(kBlock) void det_max_kernel(const void* attn, uint64_t n_attn,
+                                                         const void* gout, uint64_t n_gout,
+                                                         uint32_t* det_max) {
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  const uint64_t t0 = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  float ma = 0.f, mg = 0.f;
+  for (uint64_t i = t0; i < n_attn; i += stride) ma = fmaxf(ma, fabsf(load1<T>(attn, i)));
+  for (uint64_t i = t0; i < n_gout; i += stride) mg = fmaxf(mg, fabsf(load1<T>(gout, i)));
+  if (attn == nullptr) ma = 1.f;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    ma = fmaxf(ma, __shfl_xor(ma, d));
+    mg = fmaxf(mg, __shfl_xor(mg, d));
+  }
+  if (threadIdx.x % kWave == 0) {
+    atomicMax(&det_max[0], __float_as_uint(ma));
+    atomicMax(&det_max[1], __float_as_uint(mg));
+  }
+}
+
+// Deterministic backward, after the scatter: grad_value = acc / scale,
+// rounded once to the storage dtype.
+template <class T>
+__global__ __launch_bounds__(kBlock) void det_cast_kernel(Params p, const long long* acc,
+                                                          void* dst, uint64_t n) {
+  const double inv = 1.0 / (double)det_scale(p);
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    store1<T>(dst, i, (float)((double)acc[i] * inv));
+  }
+}
+
 int grid_for(uint64_t items) {
   // Enough workgroups to cover 256 CUs several times; grid-stride beyond.
   const uint64_t want = (items + kBlock - 1) / kBlock;
@@ -321,10 +364,52 @@ int grid_for(uint64_t items) {
 
 }  // namespace
 
-hipError_t launch_backward(int dtype, bool fp32_acc, bool fused, const Shape& s,
+hipError_t launch_backward(int dtype, AccMode acc, bool fused, const Shape& s,
                            const Params& p, hipStream_t st) {
-  return fused ? dispatch_dtype<true>(dtype, fp32_acc, s, p, st)
-               : dispatch_dtype<false>(dtype, fp32_acc, s, p, st);
+  return fused ? dispatch_dtype<true>(dtype, acc, s, p, st)
+               : dispatch_dtype<false>(dtype, acc, s, p, st);
+}
+
+hipError_t launch_det_max(int dtype, const void* attn, uint64_t n_attn, const void* grad_out,
+                          uint64_t n_gout, uint32_t* det_max, hipStream_t st) {
+  const uint64_t n = n_attn > n_gout ? n_attn : n_gout;
+  int grid = grid_for(n);
+  if (grid > 1024) grid = 1024;
+  switch (dtype) {
+    case kF32:
+      hipLaunchKernelGGL(det_max_kernel<F32>, dim3(grid), dim3(kBlock), 0, st, attn, n_attn,
+                         grad_out, n_gout, det_max);
+      break;
+    case kF16:
+      hipLaunchKernelGGL(det_max_kernel<F16>, dim3(grid), dim3(kBlock), 0, st, attn, n_attn,
+                         grad_out, n_gout, det_max);
+      break;
+    case kBF16:
+      hipLaunchKernelGGL(det_max_kernel<BF16>, dim3(grid), dim3(kBlock), 0, st, attn, n_attn,
+                         grad_out, n_gout, det_max);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_det_cast(int dtype, const Params& p, const long long* acc, void* dst,
+                           uint64_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  const int grid = grid_for(n);
+  switch (dtype) {
+    case kF32:
+      hipLaunchKernelGGL(det_cast_kernel<F32>, dim3(grid), dim3(kBlock), 0, st, p, acc, dst, n);
+      break;
+    case kF16:
+      hipLaunchKernelGGL(det_cast_kernel<F16>, dim3(grid), dim3(kBlock), 0, st, p, acc, dst, n);
+      break;
+    case kBF16:
+      hipLaunchKernelGGL(det_cast_kernel<BF16>, dim3(grid), dim3(kBlock), 0, st, p, acc, dst, n);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_ref_grad(int dtype, const Params& p, uint64_t nbq, hipStream_t st) {

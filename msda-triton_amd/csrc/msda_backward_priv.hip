@@ -33,6 +33,8 @@
 // softmax couples all L*K samples; the coupling enters only through
 // delta = <grad_out, out>, which each block computes for its queries from the
 // staged grad_out rows and the saved forward output.
+#include <type_traits>
+
 #include "msda_launch.h"
 #include "msda_scatter.h"
 
@@ -249,6 +251,8 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
   const uint32_t chb = live ? (uint32_t)(ch * CB) : kDeadLaneBytes;
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value, p.value_bytes);
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.grad_acc, p.acc_bytes);
+  constexpr bool kDet = A::kBytes == 8;  // int64 fixed point (deterministic)
+  const float det_s = kDet ? det_scale(p) : 0.f;
 
   for (int s0 = team; s0 < ns; s0 += kTeams * kUnroll) {
     uint32_t raw[kUnroll][4][kWords];
@@ -309,7 +313,7 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
           for (int c = 0; c < 4; ++c) {
             const uint16_t pos = s_pos[4 * s + c];
             if (pos != kNoPos && h_cnt[pos] < 0) {
-              Sc::add(ra, offs[c] * kAccScale, ch, p.g_real, a * w[c], sg);
+              Sc::add(ra, offs[c] * kAccScale, ch, p.g_real, a * w[c], sg, det_s);
             }
           }
         }
@@ -319,18 +323,21 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
 
   // 4. One team per shared row: sum its entries in registers, one atomic row
   //    update.  Two rows per team per step keep two LDS chains in flight.
-  //    (s_csr, h_start and s_multi were complete before step 3.)
+  //    (s_csr, h_start and s_multi were complete before step 3.)  The CSR
+  //    order of a row's entries depends on scheduling; the deterministic
+  //    variant therefore sums their int64 fixed-point values, which is exact.
+  using Acc = std::conditional_t<kDet, long long, float>;
   const int nm = n_multi;
   if (live) {
     for (int r0 = team; r0 < nm; r0 += 2 * kTeams) {
-      float acc[2][kWpl * kEpw];
+      Acc acc[2][kWpl * kEpw];
       int rows[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int ri = r0 + u * kTeams;
         rows[u] = ri < nm ? (int)s_multi[ri] : -1;
 #pragma unroll
-        for (int i = 0; i < kWpl * kEpw; ++i) acc[u][i] = 0.f;
+        for (int i = 0; i < kWpl * kEpw; ++i) acc[u][i] = 0;
         if (rows[u] < 0) continue;
         const int e1 = h_start[rows[u] + 1];
         for (int idx = h_start[rows[u]]; idx < e1; ++idx) {
@@ -345,7 +352,12 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
           for (int i = 0; i < kWpl; ++i) {
 #pragma unroll
             for (int j = 0; j < kEpw; ++j) {
-              acc[u][i * kEpw + j] += coef * gq[(ch + p.g_real * i) * kEpw + j];
+              const float v = coef * gq[(ch + p.g_real * i) * kEpw + j];
+              if constexpr (kDet) {
+                acc[u][i * kEpw + j] += to_fixed(v, det_s);
+              } else {
+                acc[u][i * kEpw + j] += v;
+              }
             }
           }
         }
@@ -356,8 +368,10 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
         const uint32_t row = h_key[rows[u]] * (uint32_t)A::kBytes;
 #pragma unroll
         for (int i = 0; i < kWpl; ++i) {
-          const uint32_t off = row + 4u * (uint32_t)(ch + p.g_real * i);
-          if constexpr (kEpw == 1) {
+          const uint32_t off = row + (uint32_t)Sc::kWordBytes * (uint32_t)(ch + p.g_real * i);
+          if constexpr (kDet) {
+            raw_buffer_atomic_add_i64(acc[u][i], ra, (int)off, 0, 0);
+          } else if constexpr (kEpw == 1) {
             atomic_add_word<A>(ra, off, acc[u][i], 0.f);
           } else {
             atomic_add_word<A>(ra, off, acc[u][2 * i], acc[u][2 * i + 1]);
@@ -403,15 +417,20 @@ hipError_t dispatch(const Shape& s, const Params& p, hipStream_t st) {
 }
 
 template <bool FUSED>
-hipError_t dispatch_dtype(int dtype, bool fp32_acc, const Shape& s, const Params& p,
+hipError_t dispatch_dtype(int dtype, AccMode acc, const Shape& s, const Params& p,
                           hipStream_t st) {
   switch (dtype) {
-    case kF32: return dispatch<F32, F32, FUSED>(s, p, st);
+    case kF32:
+      return acc == kAccI64 ? dispatch<F32, I64, FUSED>(s, p, st)
+                            : dispatch<F32, F32, FUSED>(s, p, st);
     case kF16:
-      return fp32_acc ? dispatch<F16, F32, FUSED>(s, p, st) : dispatch<F16, F16, FUSED>(s, p, st);
+      return acc == kAccI64   ? dispatch<F16, I64, FUSED>(s, p, st)
+             : acc == kAccF32 ? dispatch<F16, F32, FUSED>(s, p, st)
+                              : dispatch<F16, F16, FUSED>(s, p, st);
     case kBF16:
-      return fp32_acc ? dispatch<BF16, F32, FUSED>(s, p, st)
-                      : dispatch<BF16, BF16, FUSED>(s, p, st);
+      return acc == kAccI64   ? dispatch<BF16, I64, FUSED>(s, p, st)
+             : acc == kAccF32 ? dispatch<BF16, F32, FUSED>(s, p, st)
+                              : dispatch<BF16, BF16, FUSED>(s, p, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -435,10 +454,10 @@ void priv_params(Params* p) {
   p->nblocks = (p->npairs / (p->Q > 0 ? p->Q : 1)) * p->L * p->nqblk;
 }
 
-hipError_t launch_backward_priv(int dtype, bool fp32_acc, bool fused, const Shape& s,
+hipError_t launch_backward_priv(int dtype, AccMode acc, bool fused, const Shape& s,
                                 const Params& p, hipStream_t st) {
-  return fused ? dispatch_dtype<true>(dtype, fp32_acc, s, p, st)
-               : dispatch_dtype<false>(dtype, fp32_acc, s, p, st);
+  return fused ? dispatch_dtype<true>(dtype, acc, s, p, st)
+               : dispatch_dtype<false>(dtype, acc, s, p, st);
 }
 
 }  // namespace msda

@@ -205,11 +205,14 @@ static int forward_impl(const void* value, const int64_t* spatial_shapes,
   return MSDA_OK;
 }
 
+// det_workspace != NULL selects the deterministic backward: grad_value is
+// accumulated there as int64 fixed point (n_val * 8 bytes) followed by the
+// two max words of the scale (det_scale).
 static int backward_impl(const void* value, const int64_t* spatial_shapes,
                          const int64_t* level_start_index, const void* loc, const void* attn,
                          const void* grad_output, void* grad_value, float* grad_value_accum,
                          void* grad_loc, void* grad_attn, const Dims& d, int dtype, void* stream,
-                         const FusedArgs* f) {
+                         const FusedArgs* f, void* det_workspace = nullptr) {
   int rc = check_dims(d, dtype);
   if (rc != MSDA_OK) return rc;
   const int e = elem_bytes(dtype);
@@ -223,14 +226,24 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
   if (f && n_smp > 0 && n_out > 0 && d.S > 0 && (!f->ref || !f->lse || !f->output))
     return MSDA_ERR_INVALID_ARGUMENT;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool det = det_workspace != nullptr && n_val > 0;
   // fp32 accumulation is only a separate path for half storage.
-  const bool fp32_acc = grad_value_accum != nullptr && dtype != kF32 && n_val > 0;
-  void* acc = fp32_acc ? static_cast<void*>(grad_value_accum) : grad_value;
-  const int acc_e = fp32_acc ? 4 : e;
+  const bool fp32_acc = !det && grad_value_accum != nullptr && dtype != kF32 && n_val > 0;
+  const AccMode mode = det ? kAccI64 : fp32_acc ? kAccF32 : kAccNative;
+  void* acc = det ? det_workspace : fp32_acc ? static_cast<void*>(grad_value_accum) : grad_value;
+  const int acc_e = det ? 8 : fp32_acc ? 4 : e;
+  uint32_t* det_max =
+      det ? reinterpret_cast<uint32_t*>(static_cast<char*>(det_workspace) + n_val * 8) : nullptr;
 
-  rc = status(launch_zero(acc, (uint64_t)(n_val * acc_e), st));
+  rc = status(launch_zero(acc, (uint64_t)(n_val * acc_e) + (det ? 8u : 0u), st));
   if (rc != MSDA_OK) return rc;
   const bool compute = n_smp > 0 && n_out > 0 && d.S > 0;
+  if (det && compute) {
+    rc = status(launch_det_max(dtype, f ? nullptr : attn, f ? 0 : (uint64_t)n_smp, grad_output,
+                               (uint64_t)n_out, det_max, st));
+    if (rc != MSDA_OK) return rc;
+  }
+  const float det_samples = (float)(d.Q * d.L * d.K);
   if (n_smp > 0 && !compute) {
     // No channels or no keys: every sampled value is zero, so are the
     // location and weight gradients (and, fused, the offset, logit and
@@ -262,6 +275,8 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
       p.acc_bytes = (uint32_t)(nb * d.S * d.M * d.D * acc_e);
       p.grad_loc = at(grad_loc, so * 2, e);
       p.grad_attn = at(grad_attn, so, e);
+      p.det_max = det_max;
+      p.det_samples = det_samples;
       if (f) {
         p.ref = at(f->ref, b0 * ref_per_b, e);
         p.lse = f->lse + b0 * d.Q * d.M;
@@ -271,15 +286,23 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
       finish_params(sh, kBwdRecords, &p);
       if (bwd_priv_enabled() && priv_supported(sh, (int)d.D, (int)d.K, e)) {
         priv_params(&p);
-        rc = status(launch_backward_priv(dtype, fp32_acc, f != nullptr, sh, p, st));
+        rc = status(launch_backward_priv(dtype, mode, f != nullptr, sh, p, st));
       } else {
-        rc = status(launch_backward(dtype, fp32_acc, f != nullptr, sh, p, st));
+        rc = status(launch_backward(dtype, mode, f != nullptr, sh, p, st));
       }
       if (rc != MSDA_OK) return rc;
     }
   }
   if (fp32_acc) {
     rc = status(launch_cast(dtype, grad_value_accum, grad_value, (uint64_t)n_val, st));
+    if (rc != MSDA_OK) return rc;
+  }
+  if (det) {
+    Params p = {};
+    p.det_max = det_max;
+    p.det_samples = det_samples;
+    rc = status(launch_det_cast(dtype, p, static_cast<const long long*>(det_workspace),
+                                grad_value, (uint64_t)n_val, st));
     if (rc != MSDA_OK) return rc;
   }
   if (f && f->grad_ref) {
@@ -366,6 +389,45 @@ extern "C" int msda_fused_backward(const void* value, const int64_t* spatial_sha
                        grad_sampling_offsets, grad_attention_logits, d, dtype, stream, &f);
 }
 
+extern "C" int64_t msda_deterministic_workspace_bytes(int64_t batch, int64_t num_keys,
+                                                      int64_t num_heads, int64_t head_dim) {
+  if (batch < 0 || num_keys < 0 || num_heads < 0 || head_dim < 0) return -1;
+  return batch * num_keys * num_heads * head_dim * 8 + 64;
+}
+
+extern "C" int msda_backward_deterministic(
+    const void* value, const int64_t* spatial_shapes, const int64_t* level_start_index,
+    const void* sampling_locations, const void* attention_weights, const void* grad_output,
+    void* grad_value, void* workspace, void* grad_sampling_locations,
+    void* grad_attention_weights, int64_t batch, int64_t num_keys, int64_t num_heads,
+    int64_t head_dim, int64_t num_queries, int64_t num_levels, int64_t num_points, int dtype,
+    void* stream) {
+  const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
+  if (!workspace && batch * num_keys * num_heads * head_dim > 0) return MSDA_ERR_INVALID_ARGUMENT;
+  return backward_impl(value, spatial_shapes, level_start_index, sampling_locations,
+                       attention_weights, grad_output, grad_value, nullptr,
+                       grad_sampling_locations, grad_attention_weights, d, dtype, stream, nullptr,
+                       workspace);
+}
+
+extern "C" int msda_fused_backward_deterministic(
+    const void* value, const int64_t* spatial_shapes, const int64_t* level_start_index,
+    const void* reference_points, const void* sampling_offsets, const void* attention_logits,
+    const float* softmax_lse, const void* output, const void* grad_output, void* grad_value,
+    void* workspace, void* grad_reference_points, void* grad_sampling_offsets,
+    void* grad_attention_logits, int64_t batch, int64_t num_keys, int64_t num_heads,
+    int64_t head_dim, int64_t num_queries, int64_t num_levels, int64_t num_points,
+    int reference_levels, int dtype, void* stream) {
+  if (reference_levels != 0 && reference_levels != 1) return MSDA_ERR_INVALID_ARGUMENT;
+  const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
+  if (!workspace && batch * num_keys * num_heads * head_dim > 0) return MSDA_ERR_INVALID_ARGUMENT;
+  const FusedArgs f{reference_points, const_cast<float*>(softmax_lse), output,
+                    grad_reference_points, reference_levels};
+  return backward_impl(value, spatial_shapes, level_start_index, sampling_offsets,
+                       attention_logits, grad_output, grad_value, nullptr, grad_sampling_offsets,
+                       grad_attention_logits, d, dtype, stream, &f, workspace);
+}
+
 extern "C" const char* msda_error_string(int code) {
   switch (code) {
     case MSDA_OK: return "success";
@@ -379,4 +441,4 @@ extern "C" const char* msda_error_string(int code) {
   }
 }
 
-extern "C" int msda_abi_version(void) { return (1 << 16) | 1; }
+extern "C" int msda_abi_version(void) { return (1 << 16) | 2; }

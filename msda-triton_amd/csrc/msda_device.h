@@ -42,6 +42,10 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 __device__ bf16x2 raw_buffer_atomic_fadd_v2bf16(bf16x2 v, __amdgpu_buffer_rsrc_t rsrc,
                                                 int voffset, int soffset, int aux)
     __asm("llvm.amdgcn.raw.ptr.buffer.atomic.fadd.v2bf16");
+// 64-bit integer buffer atomic add (buffer_atomic_add_x2), bound the same way.
+__device__ long long raw_buffer_atomic_add_i64(long long v, __amdgpu_buffer_rsrc_t rsrc,
+                                               int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.atomic.add.i64");
 
 // --------------------------------------------------------------------------
 // Division by a runtime constant: n / d == (umulhi(n, mul) + n) >> shift for
@@ -71,6 +75,12 @@ struct F16 {
 struct BF16 {
   static constexpr int kBytes = 2;
   static constexpr int kCode = kBF16;
+};
+// Accumulator of the deterministic backward (int64 fixed point, see
+// det_scale); never a storage dtype.
+struct I64 {
+  static constexpr int kBytes = 8;
+  static constexpr int kCode = -1;
 };
 
 // Two storage elements packed in one 32-bit word -> two floats.
@@ -317,6 +327,8 @@ struct Params {
   const void* out_fwd;   // fused backward: the forward output (for <g, out>)
   void* grad_ref;        // fused backward: grad of the reference points
   int32_t ref_levels;    // fused: 1 if reference points are per level
+  const uint32_t* det_max;  // deterministic: bits of max|A| and max|grad_out| (>= 0)
+  float det_samples;        // deterministic: samples per (b, m) = Q * L * K
   uint32_t value_bytes;  // num_records of the value buffer
   uint32_t acc_bytes;    // num_records of the accumulator buffer
   uint32_t gout_bytes;   // num_records of grad_out
@@ -334,6 +346,30 @@ struct Params {
   int32_t nqblk;    //   query blocks per (b, m, l)
   FastDiv div_qm, div_m, div_k, div_d;
 };
+
+// Deterministic backward: grad_value is accumulated in int64 fixed point,
+// each contribution c entering as round(c * scale) with scale = 2^e, so the
+// sum is exact and independent of the order in which atomics land.  A value
+// row takes at most one corner of each sample of its (b, m), with corner
+// weights <= 1, so |grad_value[row, ch]| <= Q*L*K * max|A| * max|grad_out|;
+// e puts that bound below 2^60 (no int64 overflow, resolution bound * 2^-60).
+__device__ __forceinline__ float det_scale(const Params& p) {
+  const float bound = p.det_samples * __uint_as_float(p.det_max[0]) *
+                      __uint_as_float(p.det_max[1]);
+  int e = 100;  // bound == 0: every contribution is 0
+  if (bound > 0.f) {
+    int k = 0;
+    frexpf(bound, &k);  // bound < 2^k
+    e = 60 - k;
+  }
+  if (!(bound <= 3.0e38f)) e = -100;  // inf / NaN inputs: no overflow, result undefined
+  e = e < -100 ? -100 : (e > 100 ? 100 : e);
+  return ldexpf(1.f, e);
+}
+
+__device__ __forceinline__ long long to_fixed(float c, float scale) {
+  return (long long)rintf(c * scale);
+}
 
 // Workgroups are dispatched to the 8 XCDs round-robin (id i -> XCD i % 8).
 // Map them so that each XCD walks one contiguous range of logical blocks:

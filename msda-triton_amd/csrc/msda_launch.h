@@ -30,21 +30,32 @@ bool choose_shape(int row_bytes, int lk, int64_t npairs, bool backward, int ts_p
 // for a kernel that stages at most `max_records` samples per pass.
 void finish_params(const Shape& s, int max_records, Params* p);
 
+// grad_value accumulator of the backward: the storage dtype's own atomics,
+// an fp32 scratch, or int64 fixed point (deterministic; see det_scale).
+enum AccMode : int { kAccNative = 0, kAccF32 = 1, kAccI64 = 2 };
+
 // `fused`: the fused front-end variants (offsets + logits instead of
 // locations + weights; see Params).
 hipError_t launch_forward(int dtype, bool fused, const Shape& s, const Params& p,
                           hipStream_t st);
-hipError_t launch_backward(int dtype, bool fp32_acc, bool fused, const Shape& s,
+hipError_t launch_backward(int dtype, AccMode acc, bool fused, const Shape& s,
                            const Params& p, hipStream_t st);
 // Row-dedup backward (msda_backward_priv.hip).
 bool priv_supported(const Shape& s, int D, int K, int elem_bytes);
 void priv_params(Params* p);
-hipError_t launch_backward_priv(int dtype, bool fp32_acc, bool fused, const Shape& s,
+hipError_t launch_backward_priv(int dtype, AccMode acc, bool fused, const Shape& s,
                                 const Params& p, hipStream_t st);
 // Fused front-end: reference-point gradient from the offset gradients, one
 // wave per (b, q) of the nbq in the call.
 hipError_t launch_ref_grad(int dtype, const Params& p, uint64_t nbq, hipStream_t st);
 hipError_t launch_zero(void* ptr, uint64_t bytes, hipStream_t st);
 hipError_t launch_cast(int dtype, const float* src, void* dst, uint64_t n, hipStream_t st);
+// Deterministic backward: max|A| (or 1 for softmax weights, `attn` NULL) and
+// max|grad_out| into det_max[0..1] (zeroed beforehand), then, after the
+// backward kernel, the int64 accumulator rounded into grad_value.
+hipError_t launch_det_max(int dtype, const void* attn, uint64_t n_attn, const void* grad_out,
+                          uint64_t n_gout, uint32_t* det_max, hipStream_t st);
+hipError_t launch_det_cast(int dtype, const Params& p, const long long* acc, void* dst,
+                           uint64_t n, hipStream_t st);
 
 }  // namespace msda

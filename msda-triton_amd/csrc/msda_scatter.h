@@ -32,11 +32,17 @@ __device__ __forceinline__ void atomic_add_word(__amdgpu_buffer_rsrc_t r, uint32
 // buffer atomics per 64-byte segment, so a full segment per instruction is
 // four times faster than the 16-byte pieces a lane's own gather chunk would
 // give.  `sg` holds this lane's grad_out values in that word order.
+//
+// A = I64 (deterministic backward): each element is one 8-byte word of
+// int64 fixed point; contributions are converted with the call's scale
+// (det_scale) and added with 64-bit integer atomics, so the result does not
+// depend on their order.
 template <class T, class A, int CB>
 struct Scatter {
   static constexpr int kVec = CB / T::kBytes;
-  static constexpr int kWordsPerLane = kVec * A::kBytes / 4;  // 0: odd-D half rows
-  static constexpr int kElemsPerWord = 4 / A::kBytes;
+  static constexpr int kWordBytes = A::kBytes == 8 ? 8 : 4;
+  static constexpr int kWordsPerLane = kVec * A::kBytes / kWordBytes;  // 0: odd-D half rows
+  static constexpr int kElemsPerWord = kWordBytes / A::kBytes;
   static constexpr int kSlots = kWordsPerLane > 0 ? kWordsPerLane * kElemsPerWord : 1;
 
   // grad_out values of the words this lane scatters.
@@ -63,8 +69,15 @@ struct Scatter {
   // Add coef * sg into the row whose accumulator byte offset is `row`
   // (out-of-range rows are dropped by the buffer range check).
   __device__ __forceinline__ static void add(__amdgpu_buffer_rsrc_t r, uint32_t row, int ch,
-                                             int g_real, float coef, const float (&sg)[kSlots]) {
-    if constexpr (kWordsPerLane == 0) {
+                                             int g_real, float coef, const float (&sg)[kSlots],
+                                             float det_s = 0.f) {
+    if constexpr (A::kBytes == 8) {
+#pragma unroll
+      for (int i = 0; i < kWordsPerLane; ++i) {
+        const uint32_t off = row + 8u * (uint32_t)(ch + g_real * i);
+        raw_buffer_atomic_add_i64(to_fixed(coef * sg[i], det_s), r, (int)off, 0, 0);
+      }
+    } else if constexpr (kWordsPerLane == 0) {
       // Half storage with odd D: rows are not word aligned; add this lane's
       // element with the packed atomic on its enclosing word, zero in the
       // other half.

@@ -25,7 +25,8 @@ from torch import nn
 from torch.autograd.function import once_differentiable
 
 from . import _native
-from .ops import _DTYPE_CODE, _FLOAT_DTYPES, _use_fp32_grad_accum
+from .ops import (_DTYPE_CODE, _FLOAT_DTYPES, _use_deterministic, _use_fp32_grad_accum,
+                  deterministic_workspace)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -57,41 +58,47 @@ def fused_forward_raw(value, spatial_shapes, level_start_index, reference_points
 
 def fused_backward_raw(value, spatial_shapes, level_start_index, reference_points,
                        sampling_offsets, attention_logits, lse, out, grad_out, ref_levels: int,
-                       fp32_grad_accum: bool, need_ref_grad: bool = True):
-    """One call of ``msda_fused_backward``.  Returns ``(grad_value,
-    grad_reference_points or None, grad_offsets, grad_logits)``."""
+                       fp32_grad_accum: bool, need_ref_grad: bool = True,
+                       deterministic: bool = False):
+    """One call of ``msda_fused_backward`` (``_deterministic``).  Returns
+    ``(grad_value, grad_reference_points or None, grad_offsets, grad_logits)``."""
     B, S, M, D = value.shape
     _, Q, _, L, K, _ = sampling_offsets.shape
     grad_out = grad_out.reshape(B, Q, M, D).contiguous()
-    grad_value = torch.empty_like(value)  # zero-filled by the library
-    accum = None
-    if fp32_grad_accum and value.dtype != torch.float32:
-        accum = torch.empty(value.shape, dtype=torch.float32, device=value.device)
+    grad_value = torch.empty_like(value)  # written in full by the library
     grad_ref = torch.empty_like(reference_points) if need_ref_grad else None
     grad_off = torch.empty_like(sampling_offsets)
     grad_logits = torch.empty_like(attention_logits)
     lib = _native.load()
+    if deterministic:
+        fn, name, scratch = (lib.msda_fused_backward_deterministic,
+                             "msda_fused_backward_deterministic", deterministic_workspace(value))
+    else:
+        fn, name, scratch = lib.msda_fused_backward, "msda_fused_backward", None
+        if fp32_grad_accum and value.dtype != torch.float32:
+            scratch = torch.empty(value.shape, dtype=torch.float32, device=value.device)
     with torch.cuda.device(value.device):
-        rc = lib.msda_fused_backward(
-            _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(reference_points),
-            _ptr(sampling_offsets), _ptr(attention_logits), _ptr(lse), _ptr(out),
-            _ptr(grad_out), _ptr(grad_value), _ptr(accum), _ptr(grad_ref), _ptr(grad_off),
-            _ptr(grad_logits), B, S, M, D, Q, L, K, ref_levels, _DTYPE_CODE[value.dtype],
-            _stream(value))
-    _native.check(rc, "msda_fused_backward")
+        rc = fn(_ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(reference_points),
+                _ptr(sampling_offsets), _ptr(attention_logits), _ptr(lse), _ptr(out),
+                _ptr(grad_out), _ptr(grad_value), _ptr(scratch), _ptr(grad_ref), _ptr(grad_off),
+                _ptr(grad_logits), B, S, M, D, Q, L, K, ref_levels, _DTYPE_CODE[value.dtype],
+                _stream(value))
+    _native.check(rc, name)
     return grad_value, grad_ref, grad_off, grad_logits
 
 
 class _FusedMSDAFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, value, spatial_shapes, level_start_index, reference_points,
-                sampling_offsets, attention_logits, fp32_grad_accum, ref_levels):
+                sampling_offsets, attention_logits, fp32_grad_accum, ref_levels,
+                deterministic=False):
         out, lse = fused_forward_raw(value, spatial_shapes, level_start_index, reference_points,
                                      sampling_offsets, attention_logits, ref_levels)
         ctx.save_for_backward(value, spatial_shapes, level_start_index, reference_points,
                               sampling_offsets, attention_logits, lse, out)
         ctx.fp32_grad_accum = fp32_grad_accum
         ctx.ref_levels = ref_levels
+        ctx.deterministic = deterministic
         B, Q, M, D = out.shape
         return out.view(B, Q, M * D)
 
@@ -103,12 +110,12 @@ class _FusedMSDAFunction(torch.autograd.Function):
         gv, gref, goff, glog = fused_backward_raw(
             value, spatial_shapes, level_start_index, reference_points, sampling_offsets,
             attention_logits, lse, out, grad_out, ctx.ref_levels, ctx.fp32_grad_accum,
-            need_ref_grad=ctx.needs_input_grad[3])
-        return gv, None, None, gref, goff, glog, None, None
+            need_ref_grad=ctx.needs_input_grad[3], deterministic=ctx.deterministic)
+        return gv, None, None, gref, goff, glog, None, None, None
 
 
 def _prepare_fused(value, spatial_shapes, level_start_index, reference_points, sampling_offsets,
-                   attention_logits, fp32_grad_accum):
+                   attention_logits, fp32_grad_accum, deterministic=None):
     """Validation and defaults.  Returns the empty output for B == 0 or Q == 0,
     else the argument tuple of the device computation (logits viewed as
     (B, Q, M, L, K))."""
@@ -168,7 +175,7 @@ def _prepare_fused(value, spatial_shapes, level_start_index, reference_points, s
         fp32_grad_accum = _use_fp32_grad_accum(value)
     return (value.contiguous(), spatial_shapes, level_start_index, reference_points.contiguous(),
             sampling_offsets.contiguous(), attention_logits.contiguous(), bool(fp32_grad_accum),
-            ref_levels)
+            ref_levels, _use_deterministic(deterministic))
 
 
 def multi_scale_deformable_attention_fused(
@@ -180,6 +187,7 @@ def multi_scale_deformable_attention_fused(
     attention_logits: torch.Tensor,
     *,
     fp32_grad_accum: bool | None = None,
+    deterministic: bool | None = None,
 ) -> torch.Tensor:
     """``multi_scale_deformable_attention(value, spatial_shapes,
     level_start_index, ref + offsets / (W_l, H_l), softmax(logits))`` in one
@@ -194,14 +202,14 @@ def multi_scale_deformable_attention_fused(
         sampling_offsets: ``(B, Q, M, L, K, 2)`` in level-l pixel units.
         attention_logits: ``(B, Q, M, L, K)`` or ``(B, Q, M, L*K)``; the
             softmax runs over the L*K points of each (b, q, m).
-        fp32_grad_accum: as in ``multi_scale_deformable_attention``.
+        fp32_grad_accum, deterministic: as in ``multi_scale_deformable_attention``.
 
     Returns:
         ``(B, Q, M * D)`` in the value dtype.  Differentiable in value,
         reference_points, sampling_offsets and attention_logits.
     """
     prep = _prepare_fused(value, spatial_shapes, level_start_index, reference_points,
-                          sampling_offsets, attention_logits, fp32_grad_accum)
+                          sampling_offsets, attention_logits, fp32_grad_accum, deterministic)
     if isinstance(prep, torch.Tensor):
         return prep
     return _FusedMSDAFunction.apply(*prep)
@@ -230,7 +238,7 @@ class MSDACrossAttention(nn.Module):
         self.out_proj = nn.Linear(embed_dim, embed_dim)
 
     def forward(self, query, reference_points, value, spatial_shapes, level_start_index=None,
-                *, fp32_grad_accum=None):
+                *, fp32_grad_accum=None, deterministic=None):
         B, Q, _ = query.shape
         _, S, _ = value.shape
         M, L, K, D = self.num_heads, self.num_levels, self.num_points, self.head_dim
@@ -239,5 +247,5 @@ class MSDACrossAttention(nn.Module):
         logits = self.weight_proj(query).reshape(B, Q, M, L, K)
         out = multi_scale_deformable_attention_fused(
             v, spatial_shapes, level_start_index, reference_points, offsets, logits,
-            fp32_grad_accum=fp32_grad_accum)
+            fp32_grad_accum=fp32_grad_accum, deterministic=deterministic)
         return self.out_proj(out)

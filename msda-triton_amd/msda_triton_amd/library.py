@@ -15,13 +15,13 @@ from __future__ import annotations
 import torch
 
 from . import _native
-from .ops import _DTYPE_CODE, _prepare
+from .ops import _DTYPE_CODE, _prepare, backward_raw
 
 
 @torch.library.custom_op("msda_amd::forward", mutates_args=(), device_types="cuda")
 def _forward(value: torch.Tensor, spatial_shapes: torch.Tensor, level_start_index: torch.Tensor,
              sampling_locations: torch.Tensor, attention_weights: torch.Tensor,
-             fp32_grad_accum: bool) -> torch.Tensor:
+             fp32_grad_accum: bool, deterministic: bool) -> torch.Tensor:
     B, S, M, D = value.shape
     _, Q, _, L, K, _ = sampling_locations.shape
     out = value.new_empty(B, Q, M * D)
@@ -38,7 +38,7 @@ def _forward(value: torch.Tensor, spatial_shapes: torch.Tensor, level_start_inde
 
 @_forward.register_fake
 def _forward_fake(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
-                  fp32_grad_accum):
+                  fp32_grad_accum, deterministic):
     B, S, M, D = value.shape
     return value.new_empty(B, sampling_locations.shape[1], M * D)
 
@@ -46,40 +46,26 @@ def _forward_fake(value, spatial_shapes, level_start_index, sampling_locations, 
 @torch.library.custom_op("msda_amd::backward", mutates_args=(), device_types="cuda")
 def _backward(value: torch.Tensor, spatial_shapes: torch.Tensor, level_start_index: torch.Tensor,
               sampling_locations: torch.Tensor, attention_weights: torch.Tensor,
-              grad_output: torch.Tensor, fp32_grad_accum: bool
+              grad_output: torch.Tensor, fp32_grad_accum: bool, deterministic: bool
               ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    B, S, M, D = value.shape
-    _, Q, _, L, K, _ = sampling_locations.shape
-    grad_output = grad_output.reshape(B, Q, M, D).contiguous()
-    grad_value = torch.empty_like(value)
-    accum = (torch.empty(value.shape, dtype=torch.float32, device=value.device)
-             if fp32_grad_accum and value.dtype != torch.float32 else None)
-    grad_loc = torch.empty_like(sampling_locations)
-    grad_attn = torch.empty_like(attention_weights)
-    lib = _native.load()
-    with torch.cuda.device(value.device):
-        rc = lib.msda_backward(
-            value.data_ptr(), spatial_shapes.data_ptr(), level_start_index.data_ptr(),
-            sampling_locations.data_ptr(), attention_weights.data_ptr(), grad_output.data_ptr(),
-            grad_value.data_ptr(), None if accum is None else accum.data_ptr(),
-            grad_loc.data_ptr(), grad_attn.data_ptr(), B, S, M, D, Q, L, K,
-            _DTYPE_CODE[value.dtype], torch.cuda.current_stream(value.device).cuda_stream)
-    _native.check(rc, "msda_backward")
-    return grad_value, grad_loc, grad_attn
+    return backward_raw(value, spatial_shapes, level_start_index, sampling_locations,
+                        attention_weights, grad_output, fp32_grad_accum, deterministic)
 
 
 @_backward.register_fake
 def _backward_fake(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
-                   grad_output, fp32_grad_accum):
+                   grad_output, fp32_grad_accum, deterministic):
     return (torch.empty_like(value), torch.empty_like(sampling_locations),
             torch.empty_like(attention_weights))
 
 
 def _setup_context(ctx, inputs, output):
-    value, spatial_shapes, level_start_index, sampling_locations, attention_weights, fp32 = inputs
+    (value, spatial_shapes, level_start_index, sampling_locations, attention_weights, fp32,
+     det) = inputs
     ctx.save_for_backward(value, spatial_shapes, level_start_index, sampling_locations,
                           attention_weights)
     ctx.fp32_grad_accum = fp32
+    ctx.deterministic = det
 
 
 def _autograd_backward(ctx, grad_out):
@@ -87,8 +73,8 @@ def _autograd_backward(ctx, grad_out):
         ctx.saved_tensors)
     gv, gl, ga = torch.ops.msda_amd.backward(value, spatial_shapes, level_start_index,
                                              sampling_locations, attention_weights, grad_out,
-                                             ctx.fp32_grad_accum)
-    return gv, None, None, gl, ga, None
+                                             ctx.fp32_grad_accum, ctx.deterministic)
+    return gv, None, None, gl, ga, None, None
 
 
 torch.library.register_autograd("msda_amd::forward", _autograd_backward,
@@ -96,12 +82,12 @@ torch.library.register_autograd("msda_amd::forward", _autograd_backward,
 
 
 def msda_op(value, spatial_shapes, level_start_index, sampling_locations, attention_weights, *,
-            fp32_grad_accum: bool | None = None):
+            fp32_grad_accum: bool | None = None, deterministic: bool | None = None):
     """Same contract as `multi_scale_deformable_attention` (validation,
     defaults, empty-input early return), computed through the registered
     custom ops so that `torch.compile` captures it as one node."""
     prep = _prepare(value, spatial_shapes, level_start_index, sampling_locations,
-                    attention_weights, fp32_grad_accum)
+                    attention_weights, fp32_grad_accum, deterministic)
     if isinstance(prep, torch.Tensor):  # B == 0 or Q == 0
         return prep
     return torch.ops.msda_amd.forward(*prep)

@@ -36,6 +36,22 @@ def _use_fp32_grad_accum(value: torch.Tensor) -> bool:
     return False
 
 
+def _use_deterministic(deterministic: bool | None) -> bool:
+    """``None`` follows ``torch.use_deterministic_algorithms``: grad_value is
+    then accumulated in int64 fixed point, which makes it bitwise
+    reproducible (the other gradients always are)."""
+    if deterministic is None:
+        return torch.are_deterministic_algorithms_enabled()
+    return bool(deterministic)
+
+
+def deterministic_workspace(value: torch.Tensor) -> torch.Tensor:
+    """Scratch of the deterministic backward (int64 accumulator + scale words)."""
+    B, S, M, D = value.shape
+    nbytes = _native.load().msda_deterministic_workspace_bytes(B, S, M, D)
+    return torch.empty(nbytes, dtype=torch.uint8, device=value.device)
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -47,7 +63,7 @@ def _stream(t: torch.Tensor) -> int:
 class _MSDAFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, value, spatial_shapes, level_start_index, sampling_locations,
-                attention_weights, fp32_grad_accum):
+                attention_weights, fp32_grad_accum, deterministic=False):
         B, S, M, D = value.shape
         _, Q, _, L, K, _ = sampling_locations.shape
         lib = _native.load()
@@ -62,6 +78,7 @@ class _MSDAFunction(torch.autograd.Function):
         ctx.save_for_backward(value, spatial_shapes, level_start_index,
                               sampling_locations, attention_weights)
         ctx.fp32_grad_accum = fp32_grad_accum
+        ctx.deterministic = deterministic
         return out.view(B, Q, M * D)
 
     @staticmethod
@@ -70,27 +87,43 @@ class _MSDAFunction(torch.autograd.Function):
         value, spatial_shapes, level_start_index, sampling_locations, attention_weights = (
             ctx.saved_tensors
         )
-        B, S, M, D = value.shape
-        _, Q, _, L, K, _ = sampling_locations.shape
-        grad_out = grad_out.reshape(B, Q, M, D).contiguous()
-        lib = _native.load()
+        grad_value, grad_loc, grad_attn = backward_raw(
+            value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+            grad_out, ctx.fp32_grad_accum, ctx.deterministic)
+        return grad_value, None, None, grad_loc, grad_attn, None, None
 
-        grad_value = torch.empty_like(value)  # zero-filled by the library
-        accum = None
-        if ctx.fp32_grad_accum and value.dtype != torch.float32:
-            accum = torch.empty(value.shape, dtype=torch.float32, device=value.device)
-        grad_loc = torch.empty_like(sampling_locations)
-        grad_attn = torch.empty_like(attention_weights)
 
-        with torch.cuda.device(value.device):
+def backward_raw(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                 grad_out, fp32_grad_accum: bool, deterministic: bool):
+    """One call of ``msda_backward`` (or ``msda_backward_deterministic``) on
+    prepared tensors; returns (grad_value, grad_loc, grad_attn)."""
+    B, S, M, D = value.shape
+    _, Q, _, L, K, _ = sampling_locations.shape
+    grad_out = grad_out.reshape(B, Q, M, D).contiguous()
+    lib = _native.load()
+    grad_value = torch.empty_like(value)  # written in full by the library
+    grad_loc = torch.empty_like(sampling_locations)
+    grad_attn = torch.empty_like(attention_weights)
+    with torch.cuda.device(value.device):
+        if deterministic:
+            ws = deterministic_workspace(value)
+            rc = lib.msda_backward_deterministic(
+                _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index),
+                _ptr(sampling_locations), _ptr(attention_weights), _ptr(grad_out),
+                _ptr(grad_value), _ptr(ws), _ptr(grad_loc), _ptr(grad_attn),
+                B, S, M, D, Q, L, K, _DTYPE_CODE[value.dtype], _stream(value))
+            _native.check(rc, "msda_backward_deterministic")
+        else:
+            accum = None
+            if fp32_grad_accum and value.dtype != torch.float32:
+                accum = torch.empty(value.shape, dtype=torch.float32, device=value.device)
             rc = lib.msda_backward(
                 _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index),
                 _ptr(sampling_locations), _ptr(attention_weights), _ptr(grad_out),
                 _ptr(grad_value), _ptr(accum), _ptr(grad_loc), _ptr(grad_attn),
-                B, S, M, D, Q, L, K, _DTYPE_CODE[value.dtype], _stream(value),
-            )
-        _native.check(rc, "msda_backward")
-        return grad_value, None, None, grad_loc, grad_attn, None
+                B, S, M, D, Q, L, K, _DTYPE_CODE[value.dtype], _stream(value))
+            _native.check(rc, "msda_backward")
+    return grad_value, grad_loc, grad_attn
 
 
 def multi_scale_deformable_attention(
@@ -101,6 +134,7 @@ def multi_scale_deformable_attention(
     attention_weights: torch.Tensor,
     *,
     fp32_grad_accum: bool | None = None,
+    deterministic: bool | None = None,
 ) -> torch.Tensor:
     """Multi-scale deformable attention (Zhu et al. 2021, Eq. 1) on MI355X.
 
@@ -123,23 +157,29 @@ def multi_scale_deformable_attention(
         fp32_grad_accum: accumulate ``grad_value`` in an fp32 scratch buffer
             (rounded once to the value dtype) instead of native-dtype atomics.
             ``None`` selects the native atomics (see ``_use_fp32_grad_accum``).
+        deterministic: accumulate ``grad_value`` in int64 fixed point (exact
+            sums, bitwise reproducible; slower).  ``None`` follows
+            ``torch.are_deterministic_algorithms_enabled()``.  Overrides
+            ``fp32_grad_accum``.  Not in the reference's signature (keyword
+            only, so calls written for the reference are unaffected).
 
     Returns:
         ``(B, Q, M * D)`` output, same dtype as ``value``.
 
     Note:
-        ``grad_value`` is accumulated with atomics, so its backward is not
-        bitwise deterministic.
+        By default ``grad_value`` is accumulated with floating-point atomics,
+        so it is not bitwise deterministic (as in the reference); see
+        ``deterministic``.
     """
     prep = _prepare(value, spatial_shapes, level_start_index, sampling_locations,
-                    attention_weights, fp32_grad_accum)
+                    attention_weights, fp32_grad_accum, deterministic)
     if isinstance(prep, torch.Tensor):  # B == 0 or Q == 0: no autograd link
         return prep
     return _MSDAFunction.apply(*prep)
 
 
 def _prepare(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
-             fp32_grad_accum):
+             fp32_grad_accum, deterministic=None):
     """Validation and defaults of the operator boundary
     (src/msda_triton/ops.py:140-199).  Returns the empty output for B == 0 or
     Q == 0, else the argument tuple of the device computation."""
@@ -201,4 +241,5 @@ def _prepare(value, spatial_shapes, level_start_index, sampling_locations, atten
         sampling_locations.contiguous(),
         attention_weights.contiguous(),
         bool(fp32_grad_accum),
+        _use_deterministic(deterministic),
     )

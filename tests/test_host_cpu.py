@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_strings(lib):
-    assert lib.msda_abi_version() == (1 << 16) | 1
+    assert lib.msda_abi_version() == (1 << 16) | 2
     for code in range(5):
         assert lib.msda_error_string(code)
     assert b"unknown" in lib.msda_error_string(99)
@@ -196,11 +196,30 @@ def test_custom_ops_are_registered_with_fake_shapes():
         starts = torch.empty(2, dtype=torch.int64)
         loc = torch.empty(2, 7, 4, 2, 3, 2)
         attn = torch.empty(2, 7, 4, 2, 3)
-        out = torch.ops.msda_amd.forward(value, shapes, starts, loc, attn, False)
+        out = torch.ops.msda_amd.forward(value, shapes, starts, loc, attn, False, False)
         assert out.shape == (2, 7, 32)
         g = torch.empty(2, 7, 32)
-        gv, gl, ga = torch.ops.msda_amd.backward(value, shapes, starts, loc, attn, g, True)
+        gv, gl, ga = torch.ops.msda_amd.backward(value, shapes, starts, loc, attn, g, True, True)
         assert gv.shape == value.shape and gl.shape == loc.shape and ga.shape == attn.shape
+
+
+def test_deterministic_workspace_size(lib):
+    assert lib.msda_deterministic_workspace_bytes(4, 22223, 8, 32) == 4 * 22223 * 8 * 32 * 8 + 64
+    assert lib.msda_deterministic_workspace_bytes(-1, 1, 1, 1) == -1
+
+
+def test_deterministic_flag_follows_torch():
+    from msda_triton_amd.ops import _use_deterministic
+
+    assert _use_deterministic(True) and not _use_deterministic(False)
+    prev = torch.are_deterministic_algorithms_enabled()
+    try:
+        torch.use_deterministic_algorithms(True)
+        assert _use_deterministic(None)
+        torch.use_deterministic_algorithms(False)
+        assert not _use_deterministic(None)
+    finally:
+        torch.use_deterministic_algorithms(prev)
 
 
 def test_mmcv_shim_signature_and_validation():
