@@ -16,7 +16,8 @@ Prints ONE JSON line:
   ms_per_step  fwd+bwd wall time per step over the K timed steps
   fwd_us / bwd_us / fwd_gbps ...  per-call device times from HIP events around
                graph replays of R calls (bwd = zero-fill + backward kernel);
-               *_cold_us with L2 and Infinity Cache flushed before each call
+               *_cold_us with L2 and Infinity Cache flushed before each call;
+               bwd_deterministic_us the bitwise-reproducible backward
   roofline     backward pass (the dominant cost) vs 8 TB/s HBM
   roofline_fwd forward kernel vs 8 TB/s HBM (the operator's stated target)
   other_presets fwd / bwd / fwd+bwd device times and GB/s of the other
@@ -175,11 +176,38 @@ def preset_device_times(preset: str, lib, fp32_grad_accum: bool = False) -> dict
                                         torch.cuda.current_stream().cuda_stream), "msda_backward")
 
     f_us, b_us = _graph_us(fwd, dev), _graph_us(bwd, dev)
+    bd_us = _graph_us(deterministic_backward(lib, value, shapes, starts, loc, attn, grad_out),
+                      dev)
     fb, bb = presets.algorithmic_bytes(preset)
     return {"fwd_us": round(f_us, 2), "bwd_us": round(b_us, 2), "fwd_bwd_us": round(f_us + b_us, 2),
             "fwd_gbps": round(fb / f_us / 1e3, 1), "bwd_gbps": round(bb / b_us / 1e3, 1),
             "fwd_bwd_gbps": round((fb + bb) / (f_us + b_us) / 1e3, 1),
+            "bwd_deterministic_us": round(bd_us, 2),
             "grad_value_accum": "fp32" if accum is not None else str(value.dtype).split(".")[-1]}
+
+
+def deterministic_backward(lib, value, shapes, starts, loc, attn, grad_out):
+    """A closure calling msda_backward_deterministic (int64 fixed-point
+    grad_value) on preallocated outputs and workspace."""
+    import torch
+
+    from msda_triton_amd import _native
+    from msda_triton_amd.ops import _DTYPE_CODE, deterministic_workspace
+
+    B, S, M, D = value.shape
+    _, Q, _, L, K, _ = loc.shape
+    gv, gl, ga = torch.empty_like(value), torch.empty_like(loc), torch.empty_like(attn)
+    ws = deterministic_workspace(value, loc)
+    dt = _DTYPE_CODE[value.dtype]
+
+    def call():
+        _native.check(lib.msda_backward_deterministic(
+            value.data_ptr(), shapes.data_ptr(), starts.data_ptr(), loc.data_ptr(),
+            attn.data_ptr(), grad_out.data_ptr(), gv.data_ptr(), ws.data_ptr(), gl.data_ptr(),
+            ga.data_ptr(), B, S, M, D, Q, L, K, dt, torch.cuda.current_stream().cuda_stream),
+            "msda_backward_deterministic")
+
+    return call
 
 
 def fused_front_end_times(lib, preset: str = "decoder") -> dict:
@@ -359,6 +387,8 @@ def main() -> int:
     fwd_us = per_call_us(fwd)
     bwd_us = per_call_us(bwd)
     step_us = per_call_us(step, reps=25)
+    bwd_det_us = per_call_us(deterministic_backward(lib, value, shapes, starts, loc, attn,
+                                                    grad_out), reps=10, replays=5)
 
     # Cold variants: a 512 MiB write before every call evicts L2 and the
     # 256 MiB Infinity Cache, so the inputs come from HBM; the flush's own
@@ -428,6 +458,7 @@ def main() -> int:
         "fwd_bwd_us": round(step_us, 3),
         "fwd_gbps": round(fwd_gbps, 1),
         "bwd_gbps": round(bwd_gbps, 1),
+        "bwd_deterministic_us": round(bwd_det_us, 3),
         "fwd_cold_us": round(fwd_cold_us, 3),
         "bwd_cold_us": round(bwd_cold_us, 3),
         "api_eager_fwd_bwd_us": round(api_us, 1),

@@ -171,13 +171,15 @@ int msda_fused_backward(const void* value, const int64_t* spatial_shapes,
  * fused gradients) are deterministic in every variant.
  *
  *   workspace   device scratch of msda_deterministic_workspace_bytes(B, S, M,
- *               D) bytes (the int64 accumulator plus the scale words); its
- *               contents on entry do not matter.
+ *               D, Q, L, K, dtype) bytes (the int64 accumulator plus the scale
+ *               words; -1 for invalid sizes or dtype); its contents on entry
+ *               do not matter.
  * Other arguments as in msda_backward / msda_fused_backward (no fp32
  * accumulator: the integer accumulator replaces it).
  */
 int64_t msda_deterministic_workspace_bytes(int64_t batch, int64_t num_keys, int64_t num_heads,
-                                           int64_t head_dim);
+                                           int64_t head_dim, int64_t num_queries,
+                                           int64_t num_levels, int64_t num_points, int dtype);
 
 int msda_backward_deterministic(const void* value, const int64_t* spatial_shapes,
                                 const int64_t* level_start_index,

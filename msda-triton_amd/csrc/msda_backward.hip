@@ -322,11 +322,14 @@ __global__ __launch_bounds__(kBlock) void cast_kernel(const float* src, void* ds
 // Deterministic backward, before the scatter: max|A| (1 for softmax
 // weights, attn == NULL) and max|grad_out| into det_max[0..1].  For
 // non-negative floats the bit patterns order like the values, so an unsigned
-// integer atomicMax gives the exact maximum whatever the order.
+// integer atomicMax gives the exact maximum whatever the order.  Atomics on
+// one address serialise at the memory side, so each workgroup reduces first
+// (wave xor butterfly, then LDS) and issues one atomic per word.
 template <class T>
 __global__ __launch_bounds__(kBlock) void det_max_kernel(const void* attn, uint64_t n_attn,
                                                          const void* gout, uint64_t n_gout,
                                                          uint32_t* det_max) {
+  __shared__ float s_m[2][kBlock / kWave];
   const uint64_t stride = (uint64_t)gridDim.x * kBlock;
   const uint64_t t0 = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
   float ma = 0.f, mg = 0.f;
@@ -338,9 +341,16 @@ __global__ __launch_bounds__(kBlock) void det_max_kernel(const void* attn, uint6
     ma = fmaxf(ma, __shfl_xor(ma, d));
     mg = fmaxf(mg, __shfl_xor(mg, d));
   }
+  const int wave = threadIdx.x / kWave;
   if (threadIdx.x % kWave == 0) {
-    atomicMax(&det_max[0], __float_as_uint(ma));
-    atomicMax(&det_max[1], __float_as_uint(mg));
+    s_m[0][wave] = ma;
+    s_m[1][wave] = mg;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    float m = 0.f;
+    for (int w = 0; w < kBlock / kWave; ++w) m = fmaxf(m, s_m[threadIdx.x][w]);
+    atomicMax(&det_max[threadIdx.x], __float_as_uint(m));
   }
 }
 
@@ -374,7 +384,7 @@ hipError_t launch_det_max(int dtype, const void* attn, uint64_t n_attn, const vo
                           uint64_t n_gout, uint32_t* det_max, hipStream_t st) {
   const uint64_t n = n_attn > n_gout ? n_attn : n_gout;
   int grid = grid_for(n);
-  if (grid > 1024) grid = 1024;
+  if (grid > 256) grid = 256;
   switch (dtype) {
     case kF32:
       hipLaunchKernelGGL(det_max_kernel<F32>, dim3(grid), dim3(kBlock), 0, st, attn, n_attn,

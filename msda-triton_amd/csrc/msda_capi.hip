@@ -390,8 +390,11 @@ extern "C" int msda_fused_backward(const void* value, const int64_t* spatial_sha
 }
 
 extern "C" int64_t msda_deterministic_workspace_bytes(int64_t batch, int64_t num_keys,
-                                                      int64_t num_heads, int64_t head_dim) {
-  if (batch < 0 || num_keys < 0 || num_heads < 0 || head_dim < 0) return -1;
+                                                      int64_t num_heads, int64_t head_dim,
+                                                      int64_t num_queries, int64_t num_levels,
+                                                      int64_t num_points, int dtype) {
+  const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
+  if (check_dims(d, dtype) != MSDA_OK) return -1;
   return batch * num_keys * num_heads * head_dim * 8 + 64;
 }
 

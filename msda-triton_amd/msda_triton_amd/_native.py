@@ -32,7 +32,7 @@ SIGNATURES = {
     "msda_backward": (_INT, [_P] * 10 + [_I64] * 7 + [_INT, _P]),
     "msda_fused_forward": (_INT, [_P] * 8 + [_I64] * 7 + [_INT, _INT, _P]),
     "msda_fused_backward": (_INT, [_P] * 14 + [_I64] * 7 + [_INT, _INT, _P]),
-    "msda_deterministic_workspace_bytes": (_I64, [_I64] * 4),
+    "msda_deterministic_workspace_bytes": (_I64, [_I64] * 7 + [_INT]),
     "msda_backward_deterministic": (_INT, [_P] * 10 + [_I64] * 7 + [_INT, _P]),
     "msda_fused_backward_deterministic": (_INT, [_P] * 14 + [_I64] * 7 + [_INT, _INT, _P]),
     "msda_error_string": (ctypes.c_char_p, [_INT]),

@@ -72,7 +72,8 @@ def fused_backward_raw(value, spatial_shapes, level_start_index, reference_point
     lib = _native.load()
     if deterministic:
         fn, name, scratch = (lib.msda_fused_backward_deterministic,
-                             "msda_fused_backward_deterministic", deterministic_workspace(value))
+                             "msda_fused_backward_deterministic",
+                             deterministic_workspace(value, sampling_offsets))
     else:
         fn, name, scratch = lib.msda_fused_backward, "msda_fused_backward", None
         if fp32_grad_accum and value.dtype != torch.float32:

@@ -45,10 +45,15 @@ def _use_deterministic(deterministic: bool | None) -> bool:
     return bool(deterministic)
 
 
-def deterministic_workspace(value: torch.Tensor) -> torch.Tensor:
-    """Scratch of the deterministic backward (int64 accumulator + scale words)."""
+def deterministic_workspace(value: torch.Tensor, sampling_locations: torch.Tensor) -> torch.Tensor:
+    """Scratch of the deterministic backward (binned entries, or an int64
+    accumulator), sized by the library for this shape."""
     B, S, M, D = value.shape
-    nbytes = _native.load().msda_deterministic_workspace_bytes(B, S, M, D)
+    _, Q, _, L, K, _ = sampling_locations.shape
+    nbytes = _native.load().msda_deterministic_workspace_bytes(B, S, M, D, Q, L, K,
+                                                               _DTYPE_CODE[value.dtype])
+    if nbytes < 0:
+        raise ValueError("unsupported shape or dtype for the deterministic backward")
     return torch.empty(nbytes, dtype=torch.uint8, device=value.device)
 
 
@@ -106,7 +111,7 @@ def backward_raw(value, spatial_shapes, level_start_index, sampling_locations, a
     grad_attn = torch.empty_like(attention_weights)
     with torch.cuda.device(value.device):
         if deterministic:
-            ws = deterministic_workspace(value)
+            ws = deterministic_workspace(value, sampling_locations)
             rc = lib.msda_backward_deterministic(
                 _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index),
                 _ptr(sampling_locations), _ptr(attention_weights), _ptr(grad_out),

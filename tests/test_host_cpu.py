@@ -204,8 +204,11 @@ def test_custom_ops_are_registered_with_fake_shapes():
 
 
 def test_deterministic_workspace_size(lib):
-    assert lib.msda_deterministic_workspace_bytes(4, 22223, 8, 32) == 4 * 22223 * 8 * 32 * 8 + 64
-    assert lib.msda_deterministic_workspace_bytes(-1, 1, 1, 1) == -1
+    # int64 accumulator (8 bytes per grad_value element) + the scale words.
+    assert lib.msda_deterministic_workspace_bytes(4, 22223, 8, 32, 300, 4, 4, 2) == \
+        4 * 22223 * 8 * 32 * 8 + 64
+    assert lib.msda_deterministic_workspace_bytes(-1, 1, 1, 1, 1, 1, 1, 0) == -1
+    assert lib.msda_deterministic_workspace_bytes(1, 1, 1, 1, 1, 1, 1, 9) == -1
 
 
 def test_deterministic_flag_follows_torch():
