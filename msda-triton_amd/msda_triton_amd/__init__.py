@@ -8,17 +8,18 @@ kernels for gfx950 (libmsda_hip.so).
 from .ops import multi_scale_deformable_attention
 
 __all__ = ["multi_scale_deformable_attention", "msda_op", "MultiScaleDeformableAttnFunction",
-           "MSDeformAttnFunction", "multi_scale_deformable_attention_fused", "MSDACrossAttention"]
+           "MSDeformAttnFunction", "multi_scale_deformable_attention_fused", "MSDACrossAttention",
+           "msda_fused_op"]
 
 
 def __getattr__(name):
     # torch.library registration, the mmcv / Deformable-DETR shims and the
     # fused front-end load on first use, keeping `import msda_triton_amd` as
     # light as the reference's.
-    if name == "msda_op":
-        from .library import msda_op
+    if name in ("msda_op", "msda_fused_op"):
+        from . import library
 
-        return msda_op
+        return getattr(library, name)
     if name in ("MultiScaleDeformableAttnFunction", "MSDeformAttnFunction"):
         from . import compat
 

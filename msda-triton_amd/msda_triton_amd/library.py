@@ -91,3 +91,97 @@ def msda_op(value, spatial_shapes, level_start_index, sampling_locations, attent
     if isinstance(prep, torch.Tensor):  # B == 0 or Q == 0
         return prep
     return torch.ops.msda_amd.forward(*prep)
+
+
+# ---------------------------------------------------------------------------
+# Fused front-end (fused.py) as custom ops: forward returns (out, lse).
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("msda_amd::fused_forward", mutates_args=(), device_types="cuda")
+def _fused_forward(value: torch.Tensor, spatial_shapes: torch.Tensor,
+                   level_start_index: torch.Tensor, reference_points: torch.Tensor,
+                   sampling_offsets: torch.Tensor, attention_logits: torch.Tensor,
+                   fp32_grad_accum: bool, ref_levels: int, deterministic: bool
+                   ) -> tuple[torch.Tensor, torch.Tensor]:
+    from .fused import fused_forward_raw
+
+    out, lse = fused_forward_raw(value, spatial_shapes, level_start_index, reference_points,
+                                 sampling_offsets, attention_logits, ref_levels)
+    B, Q, M, D = out.shape
+    return out.view(B, Q, M * D), lse
+
+
+@_fused_forward.register_fake
+def _fused_forward_fake(value, spatial_shapes, level_start_index, reference_points,
+                        sampling_offsets, attention_logits, fp32_grad_accum, ref_levels,
+                        deterministic):
+    B, S, M, D = value.shape
+    Q = sampling_offsets.shape[1]
+    return (value.new_empty(B, Q, M * D),
+            value.new_empty(B, Q, M, dtype=torch.float32))
+
+
+@torch.library.custom_op("msda_amd::fused_backward", mutates_args=(), device_types="cuda")
+def _fused_backward(value: torch.Tensor, spatial_shapes: torch.Tensor,
+                    level_start_index: torch.Tensor, reference_points: torch.Tensor,
+                    sampling_offsets: torch.Tensor, attention_logits: torch.Tensor,
+                    lse: torch.Tensor, out: torch.Tensor, grad_output: torch.Tensor,
+                    fp32_grad_accum: bool, ref_levels: int, deterministic: bool
+                    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    from .fused import fused_backward_raw
+
+    B, S, M, D = value.shape
+    Q = sampling_offsets.shape[1]
+    return fused_backward_raw(value, spatial_shapes, level_start_index, reference_points,
+                              sampling_offsets, attention_logits, lse, out.view(B, Q, M, D),
+                              grad_output, ref_levels, fp32_grad_accum, need_ref_grad=True,
+                              deterministic=deterministic)
+
+
+@_fused_backward.register_fake
+def _fused_backward_fake(value, spatial_shapes, level_start_index, reference_points,
+                         sampling_offsets, attention_logits, lse, out, grad_output,
+                         fp32_grad_accum, ref_levels, deterministic):
+    return (torch.empty_like(value), torch.empty_like(reference_points),
+            torch.empty_like(sampling_offsets), torch.empty_like(attention_logits))
+
+
+def _fused_setup_context(ctx, inputs, output):
+    (value, spatial_shapes, level_start_index, reference_points, sampling_offsets,
+     attention_logits, fp32, ref_levels, det) = inputs
+    out, lse = output
+    ctx.save_for_backward(value, spatial_shapes, level_start_index, reference_points,
+                          sampling_offsets, attention_logits, lse, out)
+    ctx.fp32_grad_accum = fp32
+    ctx.ref_levels = ref_levels
+    ctx.deterministic = det
+
+
+def _fused_autograd_backward(ctx, grad_out, grad_lse):
+    del grad_lse  # the log-sum-exp is an auxiliary output
+    (value, spatial_shapes, level_start_index, reference_points, sampling_offsets,
+     attention_logits, lse, out) = ctx.saved_tensors
+    gv, gref, goff, glog = torch.ops.msda_amd.fused_backward(
+        value, spatial_shapes, level_start_index, reference_points, sampling_offsets,
+        attention_logits, lse, out, grad_out, ctx.fp32_grad_accum, ctx.ref_levels,
+        ctx.deterministic)
+    return gv, None, None, gref, goff, glog, None, None, None
+
+
+torch.library.register_autograd("msda_amd::fused_forward", _fused_autograd_backward,
+                                setup_context=_fused_setup_context)
+
+
+def msda_fused_op(value, spatial_shapes, level_start_index, reference_points, sampling_offsets,
+                  attention_logits, *, fp32_grad_accum: bool | None = None,
+                  deterministic: bool | None = None):
+    """Same contract as `multi_scale_deformable_attention_fused`, through the
+    registered custom ops (one graph node under `torch.compile`)."""
+    from .fused import _prepare_fused
+
+    prep = _prepare_fused(value, spatial_shapes, level_start_index, reference_points,
+                          sampling_offsets, attention_logits, fp32_grad_accum, deterministic)
+    if isinstance(prep, torch.Tensor):
+        return prep
+    out, _ = torch.ops.msda_amd.fused_forward(*prep)
+    return out

@@ -201,6 +201,13 @@ def test_custom_ops_are_registered_with_fake_shapes():
         g = torch.empty(2, 7, 32)
         gv, gl, ga = torch.ops.msda_amd.backward(value, shapes, starts, loc, attn, g, True, True)
         assert gv.shape == value.shape and gl.shape == loc.shape and ga.shape == attn.shape
+        ref = torch.empty(2, 7, 2, 2)
+        out, lse = torch.ops.msda_amd.fused_forward(value, shapes, starts, ref, loc, attn, False, 1,
+                                                    False)
+        assert out.shape == (2, 7, 32) and lse.shape == (2, 7, 4) and lse.dtype == torch.float32
+        grads = torch.ops.msda_amd.fused_backward(value, shapes, starts, ref, loc, attn, lse, out,
+                                                  g, False, 1, True)
+        assert [t.shape for t in grads] == [value.shape, ref.shape, loc.shape, attn.shape]
 
 
 def test_deterministic_workspace_size(lib):
