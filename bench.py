@@ -210,13 +210,9 @@ def deterministic_backward(lib, value, shapes, starts, loc, attn, grad_out):
     return call
 
 
-def fused_front_end_times(lib, preset: str = "decoder") -> dict:
-    """The fused MSDeformAttn front-end (msda_fused_forward / _backward,
-    per-level reference points) against the same front-end composed from
-    PyTorch ops around the plain operator, as the reference's attention layer
-    does it (labs/solutions/lab00.py:201-208; backward: softmax backward,
-    offset division and reference-point sum, as autograd runs them).  Both
-    graph-replayed; device time per call."""
+def fused_calls(lib, preset: str = "decoder") -> dict:
+    """Closures calling msda_fused_forward / msda_fused_backward (per-level
+    reference points) on the preset's shapes, with their buffers."""
     import torch
 
     from msda_triton_amd import _native, presets
@@ -235,18 +231,46 @@ def fused_front_end_times(lib, preset: str = "decoder") -> dict:
     goff, glog = torch.empty_like(off), torch.empty_like(logits)
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
 
-    def fused_fwd():
+    def fwd():
         _native.check(lib.msda_fused_forward(
             value.data_ptr(), shapes.data_ptr(), starts.data_ptr(), ref.data_ptr(),
             off.data_ptr(), logits.data_ptr(), out.data_ptr(), lse.data_ptr(), *dims, 1, dt,
             st()), "msda_fused_forward")
 
-    def fused_bwd():
+    def bwd():
         _native.check(lib.msda_fused_backward(
             value.data_ptr(), shapes.data_ptr(), starts.data_ptr(), ref.data_ptr(),
             off.data_ptr(), logits.data_ptr(), lse.data_ptr(), out.data_ptr(),
             grad_out.data_ptr(), gv.data_ptr(), None, gref.data_ptr(), goff.data_ptr(),
             glog.data_ptr(), *dims, 1, dt, st()), "msda_fused_backward")
+
+    return {"fwd": fwd, "bwd": bwd, "inputs": (value, shapes, starts, ref, off, logits),
+            "grad_out": grad_out, "out": out}
+
+
+def fused_front_end_times(lib, preset: str = "decoder") -> dict:
+    """The fused MSDeformAttn front-end (msda_fused_forward / _backward,
+    per-level reference points) against the same front-end composed from
+    PyTorch ops around the plain operator, as the reference's attention layer
+    does it (labs/solutions/lab00.py:201-208; backward: softmax backward,
+    offset division and reference-point sum, as autograd runs them).  Both
+    graph-replayed; device time per call."""
+    import torch
+
+    from msda_triton_amd import _native, presets
+    from msda_triton_amd.ops import _DTYPE_CODE
+
+    dev = torch.device("cuda", 0)
+    c = presets.preset_dims(preset)
+    B, S, M, D, Q, L, K = c["B"], c["S"], c["M"], c["D"], c["Q"], c["L"], c["K"]
+    f = fused_calls(lib, preset)
+    value, shapes, starts, ref, off, logits = f["inputs"]
+    grad_out, out = f["grad_out"], f["out"]
+    fused_fwd, fused_bwd = f["fwd"], f["bwd"]
+    dt = _DTYPE_CODE[value.dtype]
+    dims = (B, S, M, D, Q, L, K)
+    gv = torch.empty_like(value)
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
 
     scale = shapes.flip(-1).to(value.dtype)[None, None, None, :, None, :]
     loc = ref[:, :, None, :, None, :] + off / scale
@@ -294,8 +318,11 @@ def main() -> int:
     ap.add_argument("--no-other-presets", action="store_true",
                     help="skip the other presets and the fused front-end timings")
     ap.add_argument("--pmc-driver", action="store_true",
-                    help="for rocprofv3 --pmc runs: a few eager fwd/bwd calls plus a 256 MiB "
+                    help="for rocprofv3 runs: a few eager fwd/bwd calls plus a 256 MiB "
                          "device copy (counter calibration); prints no JSON")
+    ap.add_argument("--calls", choices=("operator", "fused", "deterministic"),
+                    default="operator",
+                    help="with --pmc-driver: which entry points the calls go through")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -348,8 +375,14 @@ def main() -> int:
         bwd()
 
     if args.pmc_driver:
+        if args.calls == "fused":
+            f = fused_calls(lib, args.preset)
+            fwd, bwd = f["fwd"], f["bwd"]
+        elif args.calls == "deterministic":
+            bwd = deterministic_backward(lib, value, shapes, starts, loc, attn, grad_out)
         for _ in range(3):
-            step()
+            fwd()
+            bwd()
         for _ in range(5):
             fwd()
         for _ in range(5):
@@ -359,7 +392,8 @@ def main() -> int:
         for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(f"pmc driver done: {args.preset}, 5 fwd, 5 bwd, 5 copies of {src.numel() * 4} bytes")
+        print(f"pmc driver done: {args.preset} ({args.calls}), 5 fwd, 5 bwd, 5 copies of "
+              f"{src.numel() * 4} bytes")
         return 0
 
     def capture(fn, reps):
@@ -459,6 +493,9 @@ def main() -> int:
         "fwd_gbps": round(fwd_gbps, 1),
         "bwd_gbps": round(bwd_gbps, 1),
         "bwd_deterministic_us": round(bwd_det_us, 3),
+        # grad_value element updates the reference's backward issues as atomics
+        # (4 corners x D per sample), per second of the whole backward call
+        "atomic_elem_per_s": round(4 * D * B * Q * M * L * K / (bwd_us * 1e-6), 1),
         "fwd_cold_us": round(fwd_cold_us, 3),
         "bwd_cold_us": round(bwd_cold_us, 3),
         "api_eager_fwd_bwd_us": round(api_us, 1),
