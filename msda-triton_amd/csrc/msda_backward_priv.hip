@@ -102,7 +102,6 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
   __shared__ float s_delta[FUSED ? kPrivSamples : 1];  // fused: <grad_out, out> per query
   __shared__ int s_wsum[4];
   __shared__ int n_multi;
-  __shared__ LevelTable lt;
 
   const int tid = threadIdx.x;
   const int D = p.D;
@@ -119,9 +118,11 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
   const int m = blk % p.M;
   const int b = blk / p.M;
   const int q0 = qb * nq;
-  const float fw = (float)p.shapes[2 * l + 1], fh = (float)p.shapes[2 * l];
+  // The block's level: read once (no LDS level table, no extra round trip).
+  const int32_t lh = (int32_t)p.shapes[2 * l], lw = (int32_t)p.shapes[2 * l + 1];
+  const int32_t lst = (int32_t)p.starts[l];
+  const float fw = (float)lw, fh = (float)lh;
 
-  load_levels(p, lt);
   for (int h = tid; h < kHashCap; h += kBlock) {
     h_key[h] = kEmpty;
     h_cnt[h] = 0;
@@ -146,17 +147,10 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
         }
       }
     }
-#pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-      const int idx = tid + it * kBlock;
-      if (idx < n) s_g[idx] = gtmp[it];
-    }
-  }
-  __syncthreads();
-
-  // 1. Stage samples; insert and count corner rows.  Lanes t and t + 128 both
-  //    build sample t's geometry and insert two of its four corners each.
-  {
+    // 1. Stage samples (their parameter loads issued together with the
+    //    grad_out loads above, one round trip), then insert and count corner
+    //    rows.  Lanes t and t + 128 both build sample t's geometry and
+    //    insert two of its four corners each.
     const int si = tid % kPrivSamples;
     const int half = tid / kPrivSamples;
     const int qi = (int)fdiv((uint32_t)si, p.div_k);
@@ -164,13 +158,20 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
     const int q = q0 + qi;
     const bool valid = si < ns && q < p.Q;
     const uint32_t pair = (uint32_t)(((int64_t)b * p.Q + q) * p.M + m);
-    const Sample smp = make_sample<T, FUSED>(p, lt, valid ? pair : 0u, (uint32_t)(l * K + k),
-                                             valid, FUSED && valid ? p.lse[pair] : 0.f);
+    const Sample smp = make_sample_at<T, FUSED>(p, valid ? pair : 0u, (uint32_t)(l * K + k),
+                                                valid, FUSED && valid ? p.lse[pair] : 0.f,
+                                                lh, lw, lst);
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int idx = tid + it * kBlock;
+      if (idx < n) s_g[idx] = gtmp[it];
+    }
     if (half == 0) {
       s_off[si] = make_uint4(smp.off[0] * T::kBytes, smp.off[1] * T::kBytes,
                              smp.off[2] * T::kBytes, smp.off[3] * T::kBytes);
       s_geo[si] = make_float4(smp.lx, smp.ly, smp.a, 0.f);
     }
+    __syncthreads();
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
       const int c = 2 * half + cc;

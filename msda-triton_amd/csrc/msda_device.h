@@ -448,6 +448,10 @@ struct Sample {
 };
 
 //
+// make_sample_at takes the sample's level (H, W, start) explicitly (kernels
+// whose workgroup covers one level read them once instead of staging a
+// table); make_sample looks them up in the workgroup's LDS level table.
+//
 // FUSED: the location is ref + offset / (W, H) (labs/solutions/lab00.py:
 // 201-207), i.e. the image coordinate x = ref_x * W + offset_x - 0.5, which
 // is evaluated in that form: one fma, exact for half-precision inputs of the
@@ -455,9 +459,9 @@ struct Sample {
 // knots), and no division.  The weight is exp(logit - lse), `lse` being the
 // pair's log-sum-exp.
 template <class T, bool FUSED = false>
-__device__ __forceinline__ Sample make_sample(const Params& p, const LevelTable& lt,
-                                              uint32_t pair, uint32_t s, bool valid,
-                                              float lse = 0.f) {
+__device__ __forceinline__ Sample make_sample_at(const Params& p, uint32_t pair, uint32_t s,
+                                                 bool valid, float lse, int32_t H, int32_t W,
+                                                 int32_t st) {
   Sample r;
   if (!valid) {
     r.off[0] = r.off[1] = r.off[2] = r.off[3] = kOobElem;
@@ -467,12 +471,11 @@ __device__ __forceinline__ Sample make_sample(const Params& p, const LevelTable&
   const uint32_t bq = fdiv(pair, p.div_m);
   const uint32_t b = fdiv(pair, p.div_qm);
   const uint32_t m = pair - bq * (uint32_t)p.M;
-  const uint32_t l = fdiv(s, p.div_k);
   const uint64_t pi = (uint64_t)pair * (uint32_t)p.LK + s;
-  const int32_t H = lt.h[l], W = lt.w[l], st = lt.start[l];
   const float fw = (float)W, fh = (float)H;
   float x, y, a;
   if constexpr (FUSED) {
+    const uint32_t l = fdiv(s, p.div_k);
     float rx, ry, ox, oy;
     load_xy<T>(p.ref, p.ref_levels ? (uint64_t)bq * (uint32_t)p.L + l : (uint64_t)bq, rx, ry);
     load_xy<T>(p.loc, pi, ox, oy);
@@ -505,6 +508,14 @@ __device__ __forceinline__ Sample make_sample(const Params& p, const LevelTable&
   r.fw = fw;
   r.fh = fh;
   return r;
+}
+
+template <class T, bool FUSED = false>
+__device__ __forceinline__ Sample make_sample(const Params& p, const LevelTable& lt,
+                                              uint32_t pair, uint32_t s, bool valid,
+                                              float lse = 0.f) {
+  const uint32_t l = valid ? fdiv(s, p.div_k) : 0u;
+  return make_sample_at<T, FUSED>(p, pair, s, valid, lse, lt.h[l], lt.w[l], lt.start[l]);
 }
 
 }  // namespace msda
