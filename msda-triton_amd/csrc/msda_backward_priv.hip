@@ -48,7 +48,11 @@ constexpr int kEntries = 4 * kPrivSamples;
 constexpr int kHashBits = 10;
 constexpr int kHashCap = 1 << kHashBits;  // >= 2x the corner entries: probing always ends
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
-constexpr int kGFloats = 2048;  // staged grad_out rows (nq * D)
+// Staged grad_out floats (nq * D): 1024 for rows of <= 32 elements, else
+// 2048.  Sized per launch shape so that the common D <= 32 case fits six
+// workgroups per CU (LDS) instead of five.
+__host__ __device__ constexpr int g_floats(int row_elems) { return row_elems <= 32 ? 1024 : 2048; }
+constexpr int kGFloatsMax = 2048;
 constexpr uint16_t kNoPos = 0xFFFF;
 constexpr int kUnroll = 4;
 
@@ -98,6 +102,7 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
   __shared__ uint16_t s_pos[kEntries];    // row of entry 4*sample+corner; kNoPos if outside
   __shared__ uint16_t s_csr[kEntries];
   __shared__ uint16_t s_multi[kEntries];  // rows with >= 2 entries
+  constexpr int kGFloats = g_floats(G * CB / T::kBytes);
   __shared__ float s_g[kGFloats];
   __shared__ float s_delta[FUSED ? kPrivSamples : 1];  // fused: <grad_out, out> per query
   __shared__ int s_wsum[4];
@@ -442,13 +447,15 @@ bool priv_supported(const Shape& s, int D, int K, int elem_bytes) {
   const int key = s.cb * 100 + s.g;
   const bool shape_ok = key == 408 || key == 416 || key == 816 || key == 1616;
   // Half storage needs word-aligned rows for the packed atomics.
-  return shape_ok && D >= 1 && D <= kGFloats && K >= 1 && K <= kPrivSamples &&
+  return shape_ok && D >= 1 && D <= g_floats(s.g * s.cb / elem_bytes) && K >= 1 &&
+         K <= kPrivSamples &&
          (D * elem_bytes) % 4 == 0;
 }
 
-void priv_params(Params* p) {
+void priv_params(const Shape& s, int elem_bytes, Params* p) {
   int nq = kPrivSamples / p->K;
-  if (nq * p->D > kGFloats) nq = kGFloats / p->D;
+  const int gf = g_floats(s.g * s.cb / elem_bytes);
+  if (nq * p->D > gf) nq = gf / p->D;
   p->nq = nq;
   p->nqblk = (p->Q + nq - 1) / nq;
   p->div_d = make_fastdiv((uint32_t)p->D);

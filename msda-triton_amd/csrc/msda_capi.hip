@@ -285,7 +285,7 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
       }
       finish_params(sh, kBwdRecords, &p);
       if (bwd_priv_enabled() && priv_supported(sh, (int)d.D, (int)d.K, e)) {
-        priv_params(&p);
+        priv_params(sh, e, &p);
         rc = status(launch_backward_priv(dtype, mode, f != nullptr, sh, p, st));
       } else {
         rc = status(launch_backward(dtype, mode, f != nullptr, sh, p, st));

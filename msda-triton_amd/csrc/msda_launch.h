@@ -42,7 +42,7 @@ hipError_t launch_backward(int dtype, AccMode acc, bool fused, const Shape& s,
                            const Params& p, hipStream_t st);
 // Row-dedup backward (msda_backward_priv.hip).
 bool priv_supported(const Shape& s, int D, int K, int elem_bytes);
-void priv_params(Params* p);
+void priv_params(const Shape& s, int elem_bytes, Params* p);
 hipError_t launch_backward_priv(int dtype, AccMode acc, bool fused, const Shape& s,
                                 const Params& p, hipStream_t st);
 // Fused front-end: reference-point gradient from the offset gradients, one
