@@ -94,11 +94,19 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
 
   // A row is identified by its hash-table position h (0..kHashCap-1).
   __shared__ uint32_t h_key[kHashCap];
-  __shared__ int h_cnt[kHashCap];        // entries per row, then CSR fill cursor / -1
-  __shared__ int h_start[kHashCap + 1];  // CSR segment of rows with >= 2 entries
+  // Entries per row, then the CSR fill cursor; dead after the fill, when the
+  // same LDS holds the per-sample results (grad_attn, grad_x, grad_y, -).
+  __shared__ union {
+    int cnt[kHashCap];
+    float4 res[kPrivSamples];
+  } u_cnt_res;
+  int* const h_cnt = u_cnt_res.cnt;
+  float4* const s_res = u_cnt_res.res;
+  // CSR segment per row (offsets <= kEntries fit 16 bits); empty for rows
+  // hit once, which are scattered directly.
+  __shared__ uint16_t h_start[kHashCap + 1];
   __shared__ uint4 s_off[kPrivSamples];
   __shared__ float4 s_geo[kPrivSamples];  // lx, ly, A, -
-  __shared__ float4 s_res[kPrivSamples];  // grad_attn, grad_x, grad_y, -
   __shared__ uint16_t s_pos[kEntries];    // row of entry 4*sample+corner; kNoPos if outside
   __shared__ uint16_t s_csr[kEntries];
   __shared__ uint16_t s_multi[kEntries];  // rows with >= 2 entries
@@ -234,12 +242,12 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * tid + i;
-      h_start[h] = base;
+      h_start[h] = (uint16_t)base;
       h_cnt[h] = mc[i] ? base : -1;  // fill cursor, or -1: single-entry row
       if (mc[i]) s_multi[atomicAdd(&n_multi, 1)] = (uint16_t)h;
       base += mc[i];
     }
-    if (tid == kBlock - 1) h_start[kHashCap] = base;
+    if (tid == kBlock - 1) h_start[kHashCap] = (uint16_t)base;
   }
   __syncthreads();
   for (int e = tid; e < kEntries; e += kBlock) {
@@ -249,8 +257,9 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
   __syncthreads();
 
   // 3. Gathers, corner dots, and the direct atomics of single-entry rows
-  //    (interleaved with the gathers, as in the direct kernel).  h_cnt now
-  //    reads -1 exactly for single-entry rows.
+  //    (interleaved with the gathers, as in the direct kernel).  A
+  //    single-entry row has an empty CSR segment; h_cnt's LDS now holds
+  //    s_res.
   const int team = tid / G;
   const int ch = tid % G;
   const bool live = ch < p.g_real;
@@ -318,7 +327,7 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             const uint16_t pos = s_pos[4 * s + c];
-            if (pos != kNoPos && h_cnt[pos] < 0) {
+            if (pos != kNoPos && h_start[pos] == h_start[pos + 1]) {  // single-entry row
               Sc::add(ra, offs[c] * kAccScale, ch, p.g_real, a * w[c], sg, det_s);
             }
           }
