@@ -60,6 +60,32 @@ __device__ __forceinline__ uint32_t hash_row(uint32_t key) {
   return (key * 2654435761u) >> (32 - kHashBits);  // Fibonacci hashing
 }
 
+// grad_out rows staged in LDS in their storage dtype (half types as raw
+// 16-bit values: no precision is lost, and the half LDS footprint lets eight
+// workgroups share a CU).
+template <class T>
+using GElem = std::conditional_t<T::kBytes == 4, float, uint16_t>;
+
+template <class T>
+__device__ __forceinline__ float g_at(const GElem<T>* g, int i) {
+  if constexpr (T::kBytes == 4) {
+    return g[i];
+  } else {
+    return unpack1<T>(g[i]);
+  }
+}
+
+// Elements i and i + 1 (i even for half storage: one 32-bit LDS read).
+template <class T>
+__device__ __forceinline__ void g_at2(const GElem<T>* g, int i, float& lo, float& hi) {
+  if constexpr (T::kBytes == 4) {
+    lo = g[i];
+    hi = g[i + 1];
+  } else {
+    unpack2<T>(*reinterpret_cast<const uint32_t*>(g + i), lo, hi);
+  }
+}
+
 // Exclusive prefix sum of v over the 256 lanes of the workgroup; `tot`
 // receives the total.  `warp_sums` holds 4 ints of LDS.
 __device__ __forceinline__ int block_exclusive_scan(int v, int* warp_sums, int* tot) {
@@ -111,7 +137,7 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
   __shared__ uint16_t s_csr[kEntries];
   __shared__ uint16_t s_multi[kEntries];  // rows with >= 2 entries
   constexpr int kGFloats = g_floats(G * CB / T::kBytes);
-  __shared__ float s_g[kGFloats];
+  __shared__ __align__(16) GElem<T> s_g[kGFloats];
   __shared__ float s_delta[FUSED ? kPrivSamples : 1];  // fused: <grad_out, out> per query
   __shared__ int s_wsum[4];
   __shared__ int n_multi;
@@ -141,22 +167,22 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
     h_cnt[h] = 0;
   }
   if (tid == 0) n_multi = 0;
-  // grad_out rows of the block's pairs in fp32 (loads batched for latency).
+  // grad_out rows of the block's pairs (loads batched for latency).
   {
     constexpr int kIt = kGFloats / kBlock;
-    float gtmp[kIt];
+    GElem<T> gtmp[kIt];
     const int n = nq * D;
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       const int idx = tid + it * kBlock;
-      gtmp[it] = 0.f;
+      gtmp[it] = 0;
       if (idx < n) {
         const int qi = (int)fdiv((uint32_t)idx, p.div_d);
         const int d = idx - qi * D;
         const int q = q0 + qi;
         if (q < p.Q) {
           const uint64_t pair = ((uint64_t)b * (uint32_t)p.Q + (uint32_t)q) * (uint32_t)p.M + m;
-          gtmp[it] = load1<T>(p.grad_out, pair * (uint32_t)D + d);
+          gtmp[it] = static_cast<const GElem<T>*>(p.grad_out)[pair * (uint32_t)D + d];
         }
       }
     }
@@ -218,7 +244,7 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
       if (qi < nq && q < p.Q) {
         const uint64_t pair = ((uint64_t)b * (uint32_t)p.Q + (uint32_t)q) * (uint32_t)p.M + m;
         for (int d = sub; d < D; d += tq) {
-          acc += s_g[qi * D + d] * load1<T>(p.out_fwd, pair * (uint32_t)D + d);
+          acc += g_at<T>(s_g, qi * D + d) * load1<T>(p.out_fwd, pair * (uint32_t)D + d);
         }
       }
       for (int x = 1; x < tq; x <<= 1) acc += __shfl_xor(acc, x);
@@ -287,10 +313,19 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
       const int s = s0 + u * kTeams;
       if (s < ns) {
         const int qi = (int)fdiv((uint32_t)s, p.div_k);
-        const float* gq = s_g + qi * D;
+        const GElem<T>* gq = s_g + qi * D;
         float gv[kVec];
+        if constexpr (T::kBytes == 2) {
 #pragma unroll
-        for (int k = 0; k < kVec; ++k) gv[k] = live ? gq[ch * kVec + k] : 0.f;
+          for (int k = 0; k < kVec; k += 2) g_at2<T>(gq, live ? ch * kVec + k : 0, gv[k], gv[k + 1]);
+        } else {
+#pragma unroll
+          for (int k = 0; k < kVec; ++k) gv[k] = g_at<T>(gq, live ? ch * kVec + k : 0);
+        }
+        if (!live) {
+#pragma unroll
+          for (int k = 0; k < kVec; ++k) gv[k] = 0.f;
+        }
         float d[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -318,8 +353,11 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
           float sg[Sc::kSlots];
 #pragma unroll
           for (int i = 0; i < kWpl; ++i) {
-#pragma unroll
-            for (int j = 0; j < kEpw; ++j) sg[i * kEpw + j] = gq[(ch + p.g_real * i) * kEpw + j];
+            if constexpr (kEpw == 2) {
+              g_at2<T>(gq, (ch + p.g_real * i) * 2, sg[2 * i], sg[2 * i + 1]);
+            } else {
+              sg[i] = g_at<T>(gq, ch + p.g_real * i);
+            }
           }
           const uint4 o = s_off[s];
           const uint32_t offs[4] = {o.x, o.y, o.z, o.w};
@@ -362,12 +400,18 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
           const float wx = (c & 1) ? geo.x : 1.f - geo.x;
           const float wy = (c & 2) ? geo.y : 1.f - geo.y;
           const float coef = geo.z * wx * wy;
-          const float* gq = s_g + (int)fdiv((uint32_t)sa, p.div_k) * D;
+          const GElem<T>* gq = s_g + (int)fdiv((uint32_t)sa, p.div_k) * D;
 #pragma unroll
           for (int i = 0; i < kWpl; ++i) {
+            float gw[kEpw];
+            if constexpr (kEpw == 2) {
+              g_at2<T>(gq, (ch + p.g_real * i) * 2, gw[0], gw[1]);
+            } else {
+              gw[0] = g_at<T>(gq, ch + p.g_real * i);
+            }
 #pragma unroll
             for (int j = 0; j < kEpw; ++j) {
-              const float v = coef * gq[(ch + p.g_real * i) * kEpw + j];
+              const float v = coef * gw[j];
               if constexpr (kDet) {
                 acc[u][i * kEpw + j] += to_fixed(v, det_s);
               } else {
