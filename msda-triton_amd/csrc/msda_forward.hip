@@ -60,8 +60,14 @@ __global__ __launch_bounds__(kBlock) void fwd_kernel(Params p) {
   const bool live = ch < p.g_real;
   const uint32_t chb = live ? (uint32_t)(ch * CB) : kDeadLaneBytes;
 
+  // Fused: when a pair's L*K logits are staged in one pass by lanes of one
+  // wave, its log-sum-exp is formed in the staging step itself (no separate
+  // prologue round trip); otherwise by pair_lse first.
+  const bool lse_inline = FUSED && p.npass == 1 && p.sch <= kWave;
   load_levels(p, lt);
-  if constexpr (FUSED) pair_lse<T>(p, pair0, ppb, team, s_lse);
+  if constexpr (FUSED) {
+    if (!lse_inline) pair_lse<T>(p, pair0, ppb, team, s_lse);
+  }
   __syncthreads();
 
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value, p.value_bytes);
@@ -78,9 +84,23 @@ __global__ __launch_bounds__(kBlock) void fwd_kernel(Params p) {
       const int jp = j >> p.log2_sch;
       const int s = pass * p.sch + (j & (p.sch - 1));
       const int pr = pair0 + jp;
-      const Sample q = make_sample<T, FUSED>(p, lt, (uint32_t)pr, (uint32_t)s,
-                                             pr < p.npairs && s < p.LK,
-                                             FUSED ? s_lse[jp] : 0.f);
+      const bool valid = pr < p.npairs && s < p.LK;
+      float lse = 0.f;
+      if constexpr (FUSED) {
+        if (lse_inline) {
+          // The pair's sch records sit on sch consecutive lanes of one wave.
+          const float x = valid ? load1<T>(p.attn, (uint64_t)pr * (uint32_t)p.LK + s) : -INFINITY;
+          float mx = x;
+          for (int d = 1; d < p.sch; d <<= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+          float z = valid ? expf(x - mx) : 0.f;
+          for (int d = 1; d < p.sch; d <<= 1) z += __shfl_xor(z, d);
+          lse = mx + logf(z);
+          if (s == 0 && pr < p.npairs && p.lse != nullptr) p.lse[pr] = lse;
+        } else {
+          lse = s_lse[jp];
+        }
+      }
+      const Sample q = make_sample<T, FUSED>(p, lt, (uint32_t)pr, (uint32_t)s, valid, lse);
       const float w1x = 1.f - q.lx, w1y = 1.f - q.ly;
       s_off[j] = make_uint4(q.off[0] * T::kBytes, q.off[1] * T::kBytes, q.off[2] * T::kBytes,
                             q.off[3] * T::kBytes);
