@@ -25,16 +25,8 @@ from torch import nn
 from torch.autograd.function import once_differentiable
 
 from . import _native
-from .ops import (_DTYPE_CODE, _FLOAT_DTYPES, _use_deterministic, _use_fp32_grad_accum,
-                  deterministic_workspace)
-
-
-def _ptr(t: torch.Tensor | None) -> int | None:
-    return None if t is None else t.data_ptr()
-
-
-def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+from .ops import (_DTYPE_CODE, _FLOAT_DTYPES, _as_index_tensor, _on_device, _ptr, _stream,
+                  _use_deterministic, _use_fp32_grad_accum, deterministic_workspace)
 
 
 def fused_forward_raw(value, spatial_shapes, level_start_index, reference_points,
@@ -47,7 +39,7 @@ def fused_forward_raw(value, spatial_shapes, level_start_index, reference_points
     lse = (torch.empty(B, Q, M, dtype=torch.float32, device=value.device)
            if need_lse else None)
     lib = _native.load()
-    with torch.cuda.device(value.device):
+    with _on_device(value):
         rc = lib.msda_fused_forward(
             _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(reference_points),
             _ptr(sampling_offsets), _ptr(attention_logits), _ptr(out), _ptr(lse),
@@ -78,7 +70,7 @@ def fused_backward_raw(value, spatial_shapes, level_start_index, reference_point
         fn, name, scratch = lib.msda_fused_backward, "msda_fused_backward", None
         if fp32_grad_accum and value.dtype != torch.float32:
             scratch = torch.empty(value.shape, dtype=torch.float32, device=value.device)
-    with torch.cuda.device(value.device):
+    with _on_device(value):
         rc = fn(_ptr(value), _ptr(spatial_shapes), _ptr(level_start_index), _ptr(reference_points),
                 _ptr(sampling_offsets), _ptr(attention_logits), _ptr(lse), _ptr(out),
                 _ptr(grad_out), _ptr(grad_value), _ptr(scratch), _ptr(grad_ref), _ptr(grad_off),
@@ -160,7 +152,7 @@ def _prepare_fused(value, spatial_shapes, level_start_index, reference_points, s
         raise ValueError("value, reference_points, sampling_offsets and attention_logits must "
                          "share a device")
 
-    spatial_shapes = spatial_shapes.to(device=value.device, dtype=torch.int64).contiguous()
+    spatial_shapes = _as_index_tensor(spatial_shapes, value.device)
     if level_start_index is None:
         hw = spatial_shapes.prod(-1)
         level_start_index = torch.cat([hw.new_zeros(1), hw.cumsum(0)[:-1]])
@@ -168,7 +160,7 @@ def _prepare_fused(value, spatial_shapes, level_start_index, reference_points, s
         if level_start_index.shape != (L,):
             raise ValueError(
                 f"level_start_index must be ({L},), got {tuple(level_start_index.shape)}")
-        level_start_index = level_start_index.to(device=value.device, dtype=torch.int64).contiguous()
+        level_start_index = _as_index_tensor(level_start_index, value.device)
 
     if B == 0 or Q == 0:
         return value.new_zeros(B, Q, M * D)

@@ -15,7 +15,7 @@ from __future__ import annotations
 import torch
 
 from . import _native
-from .ops import _DTYPE_CODE, _prepare, backward_raw
+from .ops import _DTYPE_CODE, _on_device, _prepare, _stream, backward_raw
 
 
 @torch.library.custom_op("msda_amd::forward", mutates_args=(), device_types="cuda")
@@ -26,12 +26,11 @@ def _forward(value: torch.Tensor, spatial_shapes: torch.Tensor, level_start_inde
     _, Q, _, L, K, _ = sampling_locations.shape
     out = value.new_empty(B, Q, M * D)
     lib = _native.load()
-    with torch.cuda.device(value.device):
+    with _on_device(value):
         rc = lib.msda_forward(
             value.data_ptr(), spatial_shapes.data_ptr(), level_start_index.data_ptr(),
             sampling_locations.data_ptr(), attention_weights.data_ptr(), out.data_ptr(),
-            B, S, M, D, Q, L, K, _DTYPE_CODE[value.dtype],
-            torch.cuda.current_stream(value.device).cuda_stream)
+            B, S, M, D, Q, L, K, _DTYPE_CODE[value.dtype], _stream(value))
     _native.check(rc, "msda_forward")
     return out
 

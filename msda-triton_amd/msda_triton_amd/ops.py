@@ -61,8 +61,45 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    """torch's current HIP stream on t's device, as the raw handle the C ABI
+    takes (without building a Stream object per call)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+class _on_device:
+    """The C ABI launches on the current HIP device; make t's device current
+    for the call (restoring it after), at no cost when it already is."""
+
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, t: torch.Tensor):
+        self.idx = t.device.index
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.idx:
+            self.prev = cur
+            torch.cuda.set_device(self.idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def _as_index_tensor(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    """int64, on dev, contiguous -- without a copy (or a call) when it is."""
+    if t.device != dev or t.dtype != torch.int64:
+        t = t.to(device=dev, dtype=torch.int64)
+    return t if t.is_contiguous() else t.contiguous()
 
 
 class _MSDAFunction(torch.autograd.Function):
@@ -73,7 +110,7 @@ class _MSDAFunction(torch.autograd.Function):
         _, Q, _, L, K, _ = sampling_locations.shape
         lib = _native.load()
         out = value.new_empty(B, Q, M, D)
-        with torch.cuda.device(value.device):
+        with _on_device(value):
             rc = lib.msda_forward(
                 _ptr(value), _ptr(spatial_shapes), _ptr(level_start_index),
                 _ptr(sampling_locations), _ptr(attention_weights), _ptr(out),
@@ -109,7 +146,7 @@ def backward_raw(value, spatial_shapes, level_start_index, sampling_locations, a
     grad_value = torch.empty_like(value)  # written in full by the library
     grad_loc = torch.empty_like(sampling_locations)
     grad_attn = torch.empty_like(attention_weights)
-    with torch.cuda.device(value.device):
+    with _on_device(value):
         if deterministic:
             ws = deterministic_workspace(value, sampling_locations)
             rc = lib.msda_backward_deterministic(
@@ -222,7 +259,7 @@ def _prepare(value, spatial_shapes, level_start_index, sampling_locations, atten
     if not (value.device == sampling_locations.device == attention_weights.device):
         raise ValueError("value, sampling_locations and attention_weights must share a device")
 
-    spatial_shapes = spatial_shapes.to(device=value.device, dtype=torch.int64).contiguous()
+    spatial_shapes = _as_index_tensor(spatial_shapes, value.device)
     if level_start_index is None:
         hw = spatial_shapes.prod(-1)
         level_start_index = torch.cat([hw.new_zeros(1), hw.cumsum(0)[:-1]])
@@ -231,7 +268,7 @@ def _prepare(value, spatial_shapes, level_start_index, sampling_locations, atten
             raise ValueError(
                 f"level_start_index must be ({L},), got {tuple(level_start_index.shape)}"
             )
-        level_start_index = level_start_index.to(device=value.device, dtype=torch.int64).contiguous()
+        level_start_index = _as_index_tensor(level_start_index, value.device)
 
     if B == 0 or Q == 0:
         return value.new_zeros(B, Q, M * D)
