@@ -296,12 +296,18 @@ __global__ __launch_bounds__(kBlock) void ref_grad_kernel(Params p, uint64_t nbq
 // Zero fill (a kernel rather than hipMemsetAsync so that captured graphs hold
 // only kernel nodes) and the fp32 -> dtype cast of the fp32 accumulator.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kBlock) void zero_kernel(uint4* p, uint64_t n16, uint8_t* tail,
-                                                      int ntail) {
-  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
-  for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n16; i += stride) {
+// Bytes [0, nhead) and [tail, tail + ntail) are cleared one by one (an
+// unaligned start or end), the 16-byte-aligned middle with two 16-byte stores
+// per lane and iteration (measured fastest: 7.45 us for the decoder's 45.5 MB
+// on 1024 workgroups, vs 7.9 us with one store on 8192).
+__global__ __launch_bounds__(kBlock) void zero_kernel(uint8_t* head, int nhead, uint4* p,
+                                                      uint64_t n16, uint8_t* tail, int ntail) {
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock * 2;
+  for (uint64_t i = (uint64_t)blockIdx.x * kBlock * 2 + threadIdx.x; i < n16; i += stride) {
     p[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (i + kBlock < n16) p[i + kBlock] = make_uint4(0u, 0u, 0u, 0u);
   }
+  if (blockIdx.x == 0 && (int)threadIdx.x < nhead) head[threadIdx.x] = 0;
   if (blockIdx.x == 0 && (int)threadIdx.x < ntail) tail[threadIdx.x] = 0;
 }
 
@@ -436,11 +442,16 @@ hipError_t launch_ref_grad(int dtype, const Params& p, uint64_t nbq, hipStream_t
 
 hipError_t launch_zero(void* ptr, uint64_t bytes, hipStream_t st) {
   if (bytes == 0) return hipSuccess;
-  // Torch / hipMalloc buffers are 256-byte aligned; the tail covers the rest.
-  const uint64_t n16 = bytes / 16;
-  const int ntail = (int)(bytes - n16 * 16);
-  hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n16 ? n16 : 1)), dim3(kBlock), 0, st,
-                     static_cast<uint4*>(ptr), n16, static_cast<uint8_t*>(ptr) + n16 * 16, ntail);
+  uint8_t* b = static_cast<uint8_t*>(ptr);
+  // Unaligned head (pointers into the middle of a buffer), aligned middle, tail.
+  uint64_t head = (16 - (reinterpret_cast<uintptr_t>(b) & 15)) & 15;
+  if (head > bytes) head = bytes;
+  const uint64_t n16 = (bytes - head) / 16;
+  const uint64_t ntail = bytes - head - n16 * 16;
+  uint64_t want = (n16 + 2 * kBlock - 1) / (2 * kBlock);
+  const int grid = (int)(want < 1 ? 1 : want > 1024 ? 1024 : want);
+  hipLaunchKernelGGL(zero_kernel, dim3(grid), dim3(kBlock), 0, st, b, (int)head,
+                     reinterpret_cast<uint4*>(b + head), n16, b + head + n16 * 16, (int)ntail);
   return hipGetLastError();
 }
 
