@@ -204,6 +204,54 @@ int msda_fused_backward_deterministic(const void* value, const int64_t* spatial_
                                       void* stream);
 
 /*
+ * Projections either side of the operator.  They replace the four
+ * nn.Linear calls of the reference's attention layer
+ * (labs/solutions/lab00.py:199-201 value_proj / offset_proj / weight_proj,
+ * :208 out_proj) and Deformable-DETR's masked_fill of padded value rows.
+ *
+ *   input   (rows, in_features)            dtype
+ *   weight  (split, in_features)           dtype   output columns [0, split)
+ *   weight2 (out - split, in_features)     dtype   columns [split, out); NULL if split == out
+ *   bias / bias2 (split,) / (out - split,) dtype   nullable
+ *   row_mask (rows,) uint8                 nullable; nonzero row -> output row 0
+ *   output  (rows, split), output2 (rows, out - split)
+ *
+ * output = input weight^T + bias (row_mask rows zero), fp32 accumulation, one
+ * rounding.  in_features (and, for the backward, split and out_features) must
+ * be multiples of 16 bytes of the dtype; half precision takes reductions of
+ * at most 512 (in_features forward, out_features for grad_input); the input,
+ * weight and grad_output pointers must be 16-byte aligned.  Violations return
+ * MSDA_ERR_UNSUPPORTED_SHAPE.  rows == 0 launches nothing.
+ */
+int msda_projection_forward(const void* input, const void* weight, const void* bias,
+                            const void* weight2, const void* bias2, const uint8_t* row_mask,
+                            void* output, void* output2, int64_t rows, int64_t in_features,
+                            int64_t out_features, int64_t split, int dtype, void* stream);
+
+/* Bytes of the fp32 workspace msda_projection_backward needs for weight and
+ * bias gradients (-1 for invalid arguments). */
+int64_t msda_projection_workspace_bytes(int64_t rows, int64_t in_features, int64_t out_features,
+                                        int dtype);
+
+/*
+ * Backward of msda_projection_forward.  grad_output (rows, split) and
+ * grad_output2 (rows, out - split) are the output gradients.  Every output is
+ * nullable (skipped when NULL):
+ *   grad_input   = [grad_output | grad_output2] [weight ; weight2], masked rows 0
+ *   grad_weight  = grad_output^T input over unmasked rows, grad_weight2 likewise
+ *   grad_bias    = column sums of grad_output over unmasked rows, grad_bias2 likewise
+ * Weight / bias gradients need `workspace` (msda_projection_workspace_bytes,
+ * 16-byte aligned, contents ignored); they are fixed-order sums (no atomics),
+ * so every output is bitwise reproducible.
+ */
+int msda_projection_backward(const void* input, const void* weight, const void* weight2,
+                             const uint8_t* row_mask, const void* grad_output,
+                             const void* grad_output2, void* grad_input, void* grad_weight,
+                             void* grad_bias, void* grad_weight2, void* grad_bias2,
+                             void* workspace, int64_t rows, int64_t in_features,
+                             int64_t out_features, int64_t split, int dtype, void* stream);
+
+/*
  * Human-readable text for a return code (static storage).  The reference has
  * no error channel below Python; this backs the RuntimeError that the host
  * raises for a non-zero code (src/msda_triton/ops.py:165-171 raise the

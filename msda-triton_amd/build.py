@@ -25,7 +25,10 @@ BUILD = HERE / "_build"
 OUT = HERE / "msda_triton_amd" / "libmsda_hip.so"
 ARCH = "gfx950"
 
-SOURCES = ["msda_capi.hip", "msda_forward.hip", "msda_backward.hip", "msda_backward_priv.hip"]
+SOURCES = [
+    "msda_capi.hip", "msda_forward.hip", "msda_backward.hip", "msda_backward_priv.hip",
+    "msda_proj.hip",
+]
 
 # -packed-fp32-ops off: keep v_pk_{add,mul,fma}_f32 out of the device code.
 DEVICE_FLAGS = [

@@ -431,17 +431,185 @@ extern "C" int msda_fused_backward_deterministic(
                        grad_attention_logits, d, dtype, stream, &f, workspace);
 }
 
+// ---------------------------------------------------------------------------
+// Projections either side of the operator.
+// ---------------------------------------------------------------------------
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct ProjDims {
+  int64_t rows, in, out, split;
+};
+
+// Shared argument checks.  `epu`: elements per 16 bytes; row lengths and the
+// output split must be multiples of it so every 16-byte load stays inside one
+// row of one tensor.
+static int check_proj(const ProjDims& d, int dtype) {
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return MSDA_ERR_UNSUPPORTED_DTYPE;
+  if (d.rows < 0 || d.in < 1 || d.out < 1 || d.split < 1 || d.split > d.out)
+    return MSDA_ERR_INVALID_ARGUMENT;
+  const int64_t epu = 16 / elem_bytes(dtype);
+  if (d.in % epu != 0 || d.in >= (1 << 20) || d.out >= (1 << 20) || d.rows >= (1ll << 36))
+    return MSDA_ERR_UNSUPPORTED_SHAPE;
+  if (dtype != kF32 && d.in > proj_max_reduction(dtype)) return MSDA_ERR_UNSUPPORTED_SHAPE;
+  return MSDA_OK;
+}
+
+extern "C" int msda_projection_forward(const void* input, const void* weight, const void* bias,
+                                       const void* weight2, const void* bias2,
+                                       const uint8_t* row_mask, void* output, void* output2,
+                                       int64_t rows, int64_t in_features, int64_t out_features,
+                                       int64_t split, int dtype, void* stream) {
+  const ProjDims d{rows, in_features, out_features, split};
+  int rc = check_proj(d, dtype);
+  if (rc != MSDA_OK) return rc;
+  const bool two = split < out_features;
+  if (rows == 0) return MSDA_OK;
+  if (!input || !weight || !output || (two && (!weight2 || !output2)))
+    return MSDA_ERR_INVALID_ARGUMENT;
+  if (!aligned16(input) || !aligned16(weight) || (two && !aligned16(weight2)))
+    return MSDA_ERR_UNSUPPORTED_SHAPE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int e = elem_bytes(dtype);
+  const int64_t step = dtype == kF32 ? proj_max_reduction(dtype) : in_features;
+  for (int64_t k0 = 0; k0 < in_features && rc == MSDA_OK; k0 += step) {
+    const int64_t kc = in_features - k0 < step ? in_features - k0 : step;
+    ProjArgs a{};
+    a.a0 = at(input, k0, e);
+    a.lda0 = in_features;
+    a.ksplit = (int)kc;
+    a.w0 = at(weight, k0, e);
+    a.w1 = two ? at(weight2, k0, e) : nullptr;
+    a.ldw = in_features;
+    a.b0 = k0 == 0 ? bias : nullptr;
+    a.b1 = k0 == 0 && two ? bias2 : nullptr;
+    a.mask = row_mask;
+    a.y0 = output;
+    a.y1 = two ? output2 : nullptr;
+    a.ldy0 = split;
+    a.ldy1 = out_features - split;
+    a.nsplit = (int)split;
+    a.rows = rows;
+    a.K = (int)kc;
+    a.N = (int)out_features;
+    rc = status(launch_projection(dtype, k0 > 0, a, st));
+  }
+  return rc;
+}
+
+// Workspace of the backward: the transposed weight [W; W2]^T (in x out, for
+// grad_input), then the fp32 partials of the weight / bias gradients.
+static int64_t wt_bytes(const ProjDims& d, int dtype) {
+  return (d.in * d.out * elem_bytes(dtype) + 255) / 256 * 256;
+}
+
+extern "C" int64_t msda_projection_workspace_bytes(int64_t rows, int64_t in_features,
+                                                   int64_t out_features, int dtype) {
+  const ProjDims d{rows, in_features, out_features, out_features};
+  if (check_proj(d, dtype) != MSDA_OK) return -1;
+  return wt_bytes(d, dtype) +
+         wgrad_workspace_bytes(rows, (int)out_features, (int)in_features, dtype);
+}
+
+extern "C" int msda_projection_backward(const void* input, const void* weight,
+                                        const void* weight2, const uint8_t* row_mask,
+                                        const void* grad_output, const void* grad_output2,
+                                        void* grad_input, void* grad_weight, void* grad_bias,
+                                        void* grad_weight2, void* grad_bias2, void* workspace,
+                                        int64_t rows, int64_t in_features, int64_t out_features,
+                                        int64_t split, int dtype, void* stream) {
+  const ProjDims d{rows, in_features, out_features, split};
+  int rc = check_proj(d, dtype);
+  if (rc != MSDA_OK) return rc;
+  const bool two = split < out_features;
+  const int64_t epu = 16 / elem_bytes(dtype);
+  if (split % epu != 0 || out_features % epu != 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
+  if (dtype != kF32 && out_features > proj_max_reduction(dtype) && grad_input)
+    return MSDA_ERR_UNSUPPORTED_SHAPE;
+  const bool wgrad = grad_weight || grad_bias || (two && (grad_weight2 || grad_bias2));
+  const bool dx = grad_input != nullptr && rows > 0;
+  if ((rows > 0 && (!grad_output || (two && !grad_output2))) ||
+      (dx && (!weight || (two && !weight2))) || ((dx || wgrad) && !workspace) ||
+      (wgrad && rows > 0 && !input))
+    return MSDA_ERR_INVALID_ARGUMENT;
+  if ((rows > 0 && (!aligned16(grad_output) || (two && !aligned16(grad_output2)))) ||
+      (wgrad && rows > 0 && !aligned16(input)) || ((dx || wgrad) && !aligned16(workspace)))
+    return MSDA_ERR_UNSUPPORTED_SHAPE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int e = elem_bytes(dtype);
+  char* wt = static_cast<char*>(workspace);
+  float* partials = reinterpret_cast<float*>(wt + wt_bytes(d, dtype));
+
+  // grad_input = [g | g2] [W ; W2] = [g | g2] wt^T with wt = [W ; W2]^T
+  // (in x out): proj_kernel over the output features as its reduction,
+  // segment 0 from grad_output, segment 1 from grad_output2; fp32 splits it
+  // into launches of <= 256 that accumulate.
+  if (dx) {
+    rc = status(launch_transpose(dtype, weight, two ? weight2 : nullptr, (int)split,
+                                 (int)out_features, (int)in_features, wt, st));
+    const int64_t step = dtype == kF32 ? proj_max_reduction(dtype) : out_features;
+    for (int64_t k0 = 0; k0 < out_features && rc == MSDA_OK; k0 += step) {
+      const int64_t k1 = k0 + step < out_features ? k0 + step : out_features;
+      ProjArgs a{};
+      if (k1 <= split) {
+        a.a0 = at(grad_output, k0, e);
+        a.lda0 = split;
+        a.ksplit = (int)(k1 - k0);
+      } else if (k0 >= split) {
+        a.a0 = at(grad_output2, k0 - split, e);
+        a.lda0 = out_features - split;
+        a.ksplit = (int)(k1 - k0);
+      } else {
+        a.a0 = at(grad_output, k0, e);
+        a.lda0 = split;
+        a.a1 = grad_output2;
+        a.lda1 = out_features - split;
+        a.ksplit = (int)(split - k0);
+      }
+      a.w0 = wt + k0 * e;
+      a.ldw = out_features;
+      a.mask = row_mask;
+      a.y0 = grad_input;
+      a.ldy0 = in_features;
+      a.nsplit = (int)in_features;
+      a.rows = rows;
+      a.K = (int)(k1 - k0);
+      a.N = (int)in_features;
+      rc = status(launch_projection(dtype, k0 > 0, a, st));
+    }
+  }
+  if (rc != MSDA_OK || !wgrad) return rc;
+
+  WgradArgs w{};
+  wgrad_plan(rows, (int)out_features, (int)in_features, dtype, &w);
+  w.g0 = grad_output;
+  w.g1 = two ? grad_output2 : nullptr;
+  w.ldg0 = split;
+  w.ldg1 = out_features - split;
+  w.nsplit = (int)split;
+  w.x = input;
+  w.ldx = in_features;
+  w.mask = row_mask;
+  w.ws = partials;
+  w.wsb = (grad_bias || (two && grad_bias2))
+              ? w.ws + (int64_t)w.nchunks * out_features * in_features
+              : nullptr;
+  return status(launch_wgrad(dtype, w, grad_weight, two ? grad_weight2 : nullptr, grad_bias,
+                             two ? grad_bias2 : nullptr, st));
+}
+
 extern "C" const char* msda_error_string(int code) {
   switch (code) {
     case MSDA_OK: return "success";
     case MSDA_ERR_INVALID_ARGUMENT: return "invalid argument (negative size or NULL pointer)";
     case MSDA_ERR_UNSUPPORTED_DTYPE: return "unsupported dtype (expected fp32, fp16 or bf16)";
     case MSDA_ERR_UNSUPPORTED_SHAPE:
-      return "unsupported shape (more than 64 levels, head_dim row wider than one wave, or one "
-             "batch element beyond 2^28 elements)";
+      return "unsupported shape (more than 64 levels, head_dim row wider than one wave, one "
+             "batch element beyond 2^28 elements; projections: feature counts not a multiple of "
+             "16 bytes, a half-precision reduction longer than 512, or a pointer not 16-byte "
+             "aligned)";
     case MSDA_ERR_LAUNCH: return "HIP kernel launch failed";
     default: return "unknown msda error code";
   }
 }
 
-extern "C" int msda_abi_version(void) { return (1 << 16) | 2; }
+extern "C" int msda_abi_version(void) { return (1 << 16) | 3; }

@@ -58,4 +58,57 @@ hipError_t launch_det_max(int dtype, const void* attn, uint64_t n_attn, const vo
 hipError_t launch_det_cast(int dtype, const Params& p, const long long* acc, void* dst,
                            uint64_t n, hipStream_t st);
 
+// ---------------------------------------------------------------------------
+// Projections either side of the operator (msda_proj.hip).
+// y(r, c) = sum_k A(r, k) W(c, k) (+ bias, masked rows zero); see proj_kernel.
+struct ProjArgs {
+  const void* a0;
+  const void* a1;
+  int64_t lda0, lda1;
+  int ksplit;  // reduction index k >= ksplit reads a1
+  const void* w0;
+  const void* w1;
+  int64_t ldw;
+  const void* b0;  // nullable
+  const void* b1;  // nullable
+  const uint8_t* mask;  // nullable, one byte per row
+  void* y0;
+  void* y1;
+  int64_t ldy0, ldy1;
+  int nsplit;  // output column c >= nsplit reads w1 / b1 and goes to y1
+  int64_t rows;
+  int K, N;
+  // Set per row slice by launch_projection (buffer ranges, 32-bit).
+  int nblocks;
+  uint32_t abytes0, abytes1, ybytes0, ybytes1;
+};
+// Largest reduction length one launch takes (fp32 callers split larger ones
+// into launches that accumulate).
+int proj_max_reduction(int dtype);
+hipError_t launch_projection(int dtype, bool accumulate, const ProjArgs& a, hipStream_t st);
+// wt (N x K) = [w0; w1]^T, w0 rows [0, ksplit), w1 rows [ksplit, K), both N wide.
+hipError_t launch_transpose(int dtype, const void* w0, const void* w1, int ksplit, int K, int N,
+                            void* wt, hipStream_t st);
+
+struct WgradArgs {
+  const void* g0;
+  const void* g1;
+  int64_t ldg0, ldg1;
+  int nsplit;
+  const void* x;
+  int64_t ldx;
+  const uint8_t* mask;
+  float* ws;   // [nchunks][N][K]
+  float* wsb;  // [nchunks][N], NULL: no bias gradient
+  int64_t rows;
+  int K, N;
+  int nchunks;
+  int64_t rows_per_chunk;
+  int ntile_n, ntile_k;
+};
+void wgrad_plan(int64_t rows, int n, int k, int dtype, WgradArgs* a);
+int64_t wgrad_workspace_bytes(int64_t rows, int n, int k, int dtype);
+hipError_t launch_wgrad(int dtype, const WgradArgs& a, void* dw0, void* dw1, void* db0, void* db1,
+                        hipStream_t st);
+
 }  // namespace msda

@@ -35,6 +35,9 @@ SIGNATURES = {
     "msda_deterministic_workspace_bytes": (_I64, [_I64] * 7 + [_INT]),
     "msda_backward_deterministic": (_INT, [_P] * 10 + [_I64] * 7 + [_INT, _P]),
     "msda_fused_backward_deterministic": (_INT, [_P] * 14 + [_I64] * 7 + [_INT, _INT, _P]),
+    "msda_projection_forward": (_INT, [_P] * 8 + [_I64] * 4 + [_INT, _P]),
+    "msda_projection_workspace_bytes": (_I64, [_I64] * 3 + [_INT]),
+    "msda_projection_backward": (_INT, [_P] * 12 + [_I64] * 4 + [_INT, _P]),
     "msda_error_string": (ctypes.c_char_p, [_INT]),
     "msda_abi_version": (_INT, []),
 }

@@ -214,7 +214,16 @@ class MSDACrossAttention(nn.Module):
     reference's layer (labs/solutions/lab00.py:169-208): value/offset/weight/
     output projections; offsets in each level's pixel units; softmax over all
     L*K points; ``reference_points`` ``(B, Q, 2)`` (or ``(B, Q, L, 2)``) in
-    [0, 1].  Returns ``(B, Q, C)``."""
+    [0, 1].  Returns ``(B, Q, C)``.
+
+    The four projections run on the library's MFMA projection kernels
+    (``projection.projection``): the value projection zeroes the rows flagged
+    in ``input_padding_mask`` (``(B, S)`` bool, Deformable-DETR's padded
+    pixels) in its epilogue, and the offset and logit projections share one
+    pass over the query rows.  Those kernels need ``embed_dim`` and
+    ``num_heads * num_levels * num_points`` to be multiples of 8; other
+    configurations keep the ``nn.Linear`` modules' own GEMMs (padded rows are
+    then zeroed with ``masked_fill``)."""
 
     def __init__(self, embed_dim: int, num_heads: int, num_levels: int, num_points: int):
         super().__init__()
@@ -229,16 +238,31 @@ class MSDACrossAttention(nn.Module):
         self.offset_proj = nn.Linear(embed_dim, M * L * K * 2)
         self.weight_proj = nn.Linear(embed_dim, M * L * K)
         self.out_proj = nn.Linear(embed_dim, embed_dim)
+        self.native_projections = embed_dim % 8 == 0 and (M * L * K) % 8 == 0
 
     def forward(self, query, reference_points, value, spatial_shapes, level_start_index=None,
-                *, fp32_grad_accum=None, deterministic=None):
+                *, input_padding_mask=None, fp32_grad_accum=None, deterministic=None):
         B, Q, _ = query.shape
         _, S, _ = value.shape
         M, L, K, D = self.num_heads, self.num_levels, self.num_points, self.head_dim
-        v = self.value_proj(value).reshape(B, S, M, D)
-        offsets = self.offset_proj(query).reshape(B, Q, M, L, K, 2)
-        logits = self.weight_proj(query).reshape(B, Q, M, L, K)
+        if self.native_projections:
+            from .projection import projection
+
+            v = projection(value, self.value_proj.weight, self.value_proj.bias,
+                           row_mask=input_padding_mask)
+            offsets, logits = projection(query, self.offset_proj.weight, self.offset_proj.bias,
+                                         weight2=self.weight_proj.weight,
+                                         bias2=self.weight_proj.bias)
+        else:
+            v = self.value_proj(value)
+            if input_padding_mask is not None:
+                v = v.masked_fill(input_padding_mask[..., None], 0.0)
+            offsets = self.offset_proj(query)
+            logits = self.weight_proj(query)
         out = multi_scale_deformable_attention_fused(
-            v, spatial_shapes, level_start_index, reference_points, offsets, logits,
+            v.reshape(B, S, M, D), spatial_shapes, level_start_index, reference_points,
+            offsets.reshape(B, Q, M, L, K, 2), logits.reshape(B, Q, M, L, K),
             fp32_grad_accum=fp32_grad_accum, deterministic=deterministic)
+        if self.native_projections:
+            return projection(out, self.out_proj.weight, self.out_proj.bias)
         return self.out_proj(out)

@@ -13,8 +13,13 @@ roulbac/msda-triton:
   run_reference(_fp32)    CPU upcast protocol          tests/test_msda.py:80-93
   msda_fused_reference    front-end + operator         labs/solutions/lab00.py:201-208
   run_fused_reference     its CPU upcast protocol (fwd + 4 gradients)
-Every function is pinned by tests/test_oracle.py (naive vs grid_sample in
-float64, closed forms, gradcheck, adjoint identity, planted-mistake checks).
+and (projection_reference.py) the layer's projections either side:
+  projection_reference            nn.Linear (+ masked rows)  labs/solutions/lab00.py:199-208
+  projection_backward_reference   its gradients
+Every function is pinned by tests/test_oracle.py, tests/test_oracle_fused.py
+and tests/test_oracle_projection.py (naive vs grid_sample in float64, closed
+forms, gradcheck, adjoint identity, torch's linear in float64,
+planted-mistake checks).
 """
 
 from .msda_reference import (  # noqa: F401
@@ -26,4 +31,8 @@ from .msda_reference import (  # noqa: F401
     run_fused_reference,
     run_reference,
     run_reference_fp32,
+)
+from .projection_reference import (  # noqa: F401
+    projection_backward_reference,
+    projection_reference,
 )

@@ -182,13 +182,18 @@ def test_fused_decoder_preset_full_size():
     check(out, grads, ref_out, ref_grads, torch.bfloat16)
 
 
-def test_cross_attention_layer_matches_composed_reference():
+@pytest.mark.parametrize("C,M,L,K,native", [(64, 4, 3, 4, True), (48, 2, 2, 3, False)],
+                         ids=["projection_kernels", "linear_modules"])
+@pytest.mark.parametrize("padded", [False, True], ids=["nomask", "padding_mask"])
+def test_cross_attention_layer_matches_composed_reference(C, M, L, K, native, padded):
     """The layer (projections + fused operator) against the same weights run
-    in float64 on the CPU through the oracle composition."""
+    in float64 on the CPU through the oracle composition, every parameter's
+    gradient included; with a padding mask the value rows of padded pixels
+    are zeroed after the value projection (Deformable-DETR's masked_fill)."""
     torch.manual_seed(0)
-    C, M, L, K = 64, 4, 3, 4
-    shapes_l = [(12, 16), (6, 8), (3, 4)]
+    shapes_l = [(12, 16), (6, 8), (3, 4)][:L]
     layer = MSDACrossAttention(C, M, L, K).to(DEVICE)
+    assert layer.native_projections == native
     with torch.no_grad():  # offsets of a few pixels, logits O(1)
         layer.offset_proj.weight.mul_(20.0)
     B, Q = 2, 30
@@ -197,8 +202,13 @@ def test_cross_attention_layer_matches_composed_reference():
     query = torch.randn(B, Q, C, generator=g).to(DEVICE).requires_grad_(True)
     value = torch.randn(B, S, C, generator=g).to(DEVICE).requires_grad_(True)
     refp = torch.rand(B, Q, 2, generator=g).to(DEVICE).requires_grad_(True)
+    mask = None
+    if padded:
+        mask = torch.rand(B, S, generator=g) < 0.3
+        mask[1, S // 2:] = True
+        mask = mask.to(DEVICE)
     shapes = torch.tensor(shapes_l, device=DEVICE)
-    out = layer(query, refp, value, shapes)
+    out = layer(query, refp, value, shapes, input_padding_mask=mask)
     gout = torch.randn(out.shape, generator=g).to(DEVICE)
     out.backward(gout)
 
@@ -208,17 +218,21 @@ def test_cross_attention_layer_matches_composed_reference():
     v64 = value.detach().double().cpu().requires_grad_(True)
     r64 = refp.detach().double().cpu().requires_grad_(True)
     D = C // M
-    vv = cpu.value_proj(v64).reshape(B, S, M, D)
+    vv = cpu.value_proj(v64)
+    if padded:
+        vv = vv.masked_fill(mask.cpu()[..., None], 0.0)
+    vv = vv.reshape(B, S, M, D)
     offs = cpu.offset_proj(q64).reshape(B, Q, M, L, K, 2)
     logits = cpu.weight_proj(q64).reshape(B, Q, M, L, K)
     ref_out = cpu.out_proj(msda_fused_reference(vv, shapes.cpu(), r64, offs, logits))
     ref_out.backward(gout.double().cpu())
     assert rel_err(out, ref_out) <= 1e-5
-    for name, a, b in (("query", query.grad, q64.grad), ("value", value.grad, v64.grad),
-                       ("reference_points", refp.grad, r64.grad),
-                       ("offset_proj.weight", layer.offset_proj.weight.grad,
-                        cpu.offset_proj.weight.grad),
-                       ("weight_proj.weight", layer.weight_proj.weight.grad,
-                        cpu.weight_proj.weight.grad)):
+    checks = [("query", query.grad, q64.grad), ("value", value.grad, v64.grad),
+              ("reference_points", refp.grad, r64.grad)]
+    for mod in ("value_proj", "offset_proj", "weight_proj", "out_proj"):
+        for par in ("weight", "bias"):
+            checks.append((f"{mod}.{par}", getattr(getattr(layer, mod), par).grad,
+                           getattr(getattr(cpu, mod), par).grad))
+    for name, a, b in checks:
         e = rel_err(a, b)
         assert e <= 1e-4, f"{name}: rel_err {e:.3e}"

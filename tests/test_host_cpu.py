@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_strings(lib):
-    assert lib.msda_abi_version() == (1 << 16) | 2
+    assert lib.msda_abi_version() == (1 << 16) | 3
     for code in range(5):
         assert lib.msda_error_string(code)
     assert b"unknown" in lib.msda_error_string(99)
