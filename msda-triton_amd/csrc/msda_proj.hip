@@ -72,19 +72,26 @@ __device__ __forceinline__ int acc_row(int i, int slot) { return (i >> 2) * 8 + 
 // W(c, k): c <  nsplit -> w0[c*ldw + k], else w1[(c-nsplit)*ldw + k]
 // y(r, c): c <  nsplit -> y0[r*ldy0 + c], else y1[r*ldy1 + c - nsplit]  (SPLITN)
 //
-// Persistent workgroups of 4 waves; a workgroup owns 4*32*TILES output columns
-// (grid.y) and walks row blocks of 32 (grid.x stride).  Each wave keeps its
-// 32*TILES weight columns x KP in registers for the whole kernel (KP = NU*UK,
-// zero past K, so the MFMA loop has a fixed trip count).  The 32 x KP
-// activation block is loaded with 16-byte row-contiguous buffer loads two
-// blocks ahead (registers), parked in LDS (two buffers, one barrier per
-// block) and read back as MFMA fragments.  Every load and store is a buffer
-// access whose range check turns rows past the end into zero reads and
-// dropped writes: the instruction stream is the same for every block, so the
-// compiler's wait counts stay exact and the prefetch really overlaps.  The
-// row mask of a block travels as one 32-bit word (wave 0's ballot).  Output:
-// lanes 2m, 2m+1 hold columns c, c+1; one DPP swap per row pair lets each
-// lane store two adjacent columns of one row (8 stores per 32x32 tile).
+// Persistent workgroups of 4 waves; a workgroup owns 128 output columns
+// (grid.y) and walks row blocks of 32 (grid.x stride); the column groups of
+// one row block run on the same XCD (linear ids differ by a multiple of 8),
+// so the second read of the block hits L2.  Each wave keeps its 32 weight
+// columns x KP in registers for the whole kernel (KP = NU*UK, zero past K, so
+// the MFMA loop has a fixed trip count): 64 registers for K <= 256 in half
+// precision, and three workgroups share a CU.
+//
+// LDS rows are KP*E bytes, unpadded; 16-byte chunk c of row r sits at chunk
+// position c ^ (r & 15), so the 16 rows a quarter-wave reads for one MFMA
+// fragment fall on 16 distinct 4-bank groups.  The weights enter through the
+// same buffers once (coalesced row loads).  Activation blocks are copied from
+// memory straight into LDS (buffer_load_dwordx4 ... lds, one block ahead, two
+// buffers, one barrier per block) -- no staging registers; with SPLITA the
+// two source tensors need per-lane descriptors, so that variant stages through
+// registers instead.  Buffer range checks turn rows past the end into zero
+// reads and dropped stores, so every block issues the same instructions.
+// The row mask of a block travels as one 32-bit word (wave 0's ballot).
+// Output: lanes 2m, 2m+1 hold columns c, c+1; one DPP swap per row pair lets
+// each lane store two adjacent columns of one row.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kOob = 0x80000000u;  // beyond any num_records used here
 
@@ -114,19 +121,34 @@ __device__ __forceinline__ float swap_pair_lane(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
 }
 
-template <class T, int TILES, bool ACC, bool SPLITA, bool SPLITN>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__device__ __forceinline__ int swz(int r, int c) { return c ^ (r & 15); }
+
+template <int NU, bool SPLITA>
+constexpr int proj_waves_per_eu() {
+  return NU == 16 ? 3 : 2;
+}
+
+template <class T, int NU, bool ACC, bool SPLITA, bool SPLITN>
+__global__ __launch_bounds__(kBlock)
+__attribute__((amdgpu_waves_per_eu(proj_waves_per_eu<NU, SPLITA>())))
 void proj_kernel(ProjArgs p) {
   constexpr int E = T::kBytes;
-  constexpr int EPU = 16 / E;    // elements per lane per unit
-  constexpr int UK = 2 * EPU;    // k covered by one unit
-  constexpr int NU = 32 / TILES; // units per row (K <= NU * UK)
+  constexpr int EPU = 16 / E;          // elements per lane per unit
+  constexpr int UK = 2 * EPU;          // k covered by one unit
   constexpr int KP = NU * UK;
-  constexpr int PITCH = KP * E + 16;
-  constexpr int CPR = KP * E / 16;           // 16-byte chunks per staged row
-  constexpr int ROUNDS = 32 * CPR / kBlock;  // loads per thread per block
-  constexpr int BUF = 32 * PITCH + 16;
-  __shared__ __align__(16) unsigned char smem[2 * BUF];
+  constexpr int ROWB = KP * E;         // LDS bytes per row
+  constexpr int CPR = ROWB / 16;       // 16-byte chunks per row
+  constexpr int BUFB = 32 * ROWB;      // one 32-row block
+  constexpr int IPW = BUFB / 1024 / 4; // 1 KB direct-to-LDS loads per wave per block
+  constexpr int ROUNDS = 32 * CPR / kBlock;
+  // Half-precision outputs (K <= 256) leave through an LDS tile: each wave
+  // parks its 32 x 32 results, then every lane stores 16-byte row chunks of
+  // the workgroup's 32 x 128 block (full 256-byte row segments).
+  constexpr bool WIDE = E == 2 && NU == 16;
+  constexpr int OPITCH = 128 * E + 16;
+  __shared__ __align__(16) unsigned char smem[2 * BUFB];
+  __shared__ __align__(16) unsigned char sout[WIDE ? 2 : 1][WIDE ? 32 * OPITCH : 16];
+  __shared__ uint32_t smask[2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -139,105 +161,169 @@ void proj_kernel(ProjArgs p) {
   const __amdgpu_buffer_rsrc_t ry1 = make_rsrc(SPLITN ? p.y1 : p.y0, SPLITN ? p.ybytes1 : 0u);
   const __amdgpu_buffer_rsrc_t rmask = make_rsrc(p.mask, p.mask != nullptr ? (uint32_t)p.rows : 0u);
 
-  // ---- weights and bias -> registers ----
-  const int col0 = (blockIdx.y * 4 + wave) * 32 * TILES;
-  i32x4 w[TILES][NU];
-  float bias[TILES];
-#pragma unroll
-  for (int t = 0; t < TILES; ++t) {
-    const int c = col0 + 32 * t + rl;
-    const bool hi = c >= p.nsplit;
-    const int64_t cc = hi ? c - p.nsplit : c;
-    const char* base = static_cast<const char*>(hi ? p.w1 : p.w0) + cc * p.ldw * E;
-    const void* bp = hi ? p.b1 : p.b0;
-    bias[t] = (c < p.N && bp != nullptr) ? load1<T>(bp, (uint64_t)cc) : 0.f;
-#pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const int k = UK * u + EPU * slot;
-      w[t][u] = (c < p.N && k < p.K) ? ld16(base + k * E) : i32x4{0, 0, 0, 0};
+  // ---- weights -> registers: two passes of 64 weight rows through LDS ----
+  // Loads are coalesced row chunks; for NU == 16 both passes' loads are issued
+  // before the first LDS pass (one memory latency for the whole prologue).
+  const int colw = blockIdx.y * 128;  // first output column of this workgroup
+  const int col0 = colw + wave * 32;  // ... of this wave
+  constexpr int WQ = 2 * ROUNDS;      // loads per thread per pass
+  auto wload = [&](int pass, int q) {
+    const int idx = tid + kBlock * q;
+    const int r = idx / CPR;  // 0..63
+    const int ch = idx - r * CPR;
+    const int c = colw + pass * 64 + r;
+    const int k = ch * EPU;
+    i32x4 v = i32x4{0, 0, 0, 0};
+    if (c < p.N && k < p.K) {
+      const bool hi = c >= p.nsplit;
+      const char* base = static_cast<const char*>(hi ? p.w1 : p.w0);
+      v = ld16(base + ((int64_t)(hi ? c - p.nsplit : c) * p.ldw + k) * E);
     }
-  }
-
-  // ---- activation staging (two blocks in flight) ----
-  // Rows are clamped to p.rows, whose offsets lie at or past num_records.
-  i32x4 pre[2][ROUNDS];
-  uint32_t pre_mask[2] = {0u, 0u};
-  auto load_block = [&](int pb, int blk) {
-    const int r0 = blk * 32;
+    return v;
+  };
+  auto wpark = [&](int q, const i32x4& v) {
+    const int idx = tid + kBlock * q;
+    const int r = idx / CPR;
+    const int ch = idx - r * CPR;
+    *reinterpret_cast<i32x4*>(smem + r * ROWB + swz(r, ch) * 16) = v;
+  };
+  i32x4 w[NU];
+  auto wpick = [&](int pass) {
+    __syncthreads();
+    if ((wave >> 1) == pass) {
+      const int r = (wave & 1) * 32 + rl;
 #pragma unroll
-    for (int q = 0; q < ROUNDS; ++q) {
-      const int idx = tid + kBlock * q;
-      const int r = idx / CPR;
-      const int k = (idx - r * CPR) * EPU;
-      const uint32_t row = (uint32_t)min(r0 + r, nrows);
-      if constexpr (SPLITA) {
-        const uint32_t o0 = k < p.ksplit ? (row * lda0 + k) * E : kOob;
-        const uint32_t o1 = (k >= p.ksplit && k < p.K) ? (row * lda1 + k - p.ksplit) * E : kOob;
-        pre[pb][q] = __builtin_amdgcn_raw_buffer_load_b128(ra0, o0, 0, 0) |
-                     __builtin_amdgcn_raw_buffer_load_b128(ra1, o1, 0, 0);
-      } else {
-        const uint32_t o0 = k < p.K ? (row * lda0 + k) * E : kOob;
-        pre[pb][q] = __builtin_amdgcn_raw_buffer_load_b128(ra0, o0, 0, 0);
+      for (int u = 0; u < NU; ++u) {
+        w[u] = *reinterpret_cast<const i32x4*>(smem + r * ROWB + swz(r, 2 * u + slot) * 16);
       }
     }
-    pre_mask[pb] = (wave == 0 && lane < 32)
-                       ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(
-                             rmask, (uint32_t)min(r0 + lane, nrows), 0, 0)
-                       : 0u;
+    __syncthreads();
+  };
+  if constexpr (NU == 16) {
+    i32x4 st0[WQ], st1[WQ];
+#pragma unroll
+    for (int q = 0; q < WQ; ++q) st0[q] = wload(0, q);
+#pragma unroll
+    for (int q = 0; q < WQ; ++q) st1[q] = wload(1, q);
+#pragma unroll
+    for (int q = 0; q < WQ; ++q) wpark(q, st0[q]);
+    wpick(0);
+#pragma unroll
+    for (int q = 0; q < WQ; ++q) wpark(q, st1[q]);
+    wpick(1);
+  } else {
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+      for (int q = 0; q < WQ; ++q) wpark(q, wload(pass, q));
+      wpick(pass);
+    }
+  }
+  const int c_lane = col0 + rl;
+  float bias = 0.f;
+  {
+    const bool hi = c_lane >= p.nsplit;
+    const void* bp = hi ? p.b1 : p.b0;
+    if (c_lane < p.N && bp != nullptr) bias = load1<T>(bp, (uint64_t)(hi ? c_lane - p.nsplit : c_lane));
+  }
+
+  // ---- activation blocks ----
+  // Rows are clamped to nrows, whose offsets lie at or past num_records.
+  i32x4 pre[SPLITA ? ROUNDS : 1];
+  uint32_t pre_mask = 0u;
+  auto issue_block = [&](int pb, int blk) {
+    const int r0 = blk * 32;
+    unsigned char* b = smem + pb * BUFB;
+    if constexpr (!SPLITA) {
+#pragma unroll
+      for (int j = 0; j < IPW; ++j) {
+        const int byte = (wave * IPW + j) * 1024 + lane * 16;
+        const int r = byte / ROWB;
+        const int c = swz(r, (byte - r * ROWB) / 16);
+        const int k = c * EPU;
+        const uint32_t row = (uint32_t)min(r0 + r, nrows);
+        const uint32_t off = k < p.K ? (row * lda0 + k) * E : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra0, b + (wave * IPW + j) * 1024, 16, off, 0, 0,
+                                                 0);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < ROUNDS; ++q) {
+        const int idx = tid + kBlock * q;
+        const int r = idx / CPR;
+        const int k = (idx - r * CPR) * EPU;
+        const uint32_t row = (uint32_t)min(r0 + r, nrows);
+        const uint32_t o0 = k < p.ksplit ? (row * lda0 + k) * E : kOob;
+        const uint32_t o1 = (k >= p.ksplit && k < p.K) ? (row * lda1 + k - p.ksplit) * E : kOob;
+        pre[q] = __builtin_amdgcn_raw_buffer_load_b128(ra0, o0, 0, 0) |
+                 __builtin_amdgcn_raw_buffer_load_b128(ra1, o1, 0, 0);
+      }
+    }
+    pre_mask = (wave == 0 && lane < 32)
+                   ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(
+                         rmask, (uint32_t)min(r0 + lane, nrows), 0, 0)
+                   : 0u;
+  };
+  // SPLITA only: registers -> LDS (swizzled), before the block's barrier.
+  auto park_block = [&](int pb) {
+    if constexpr (SPLITA) {
+      unsigned char* b = smem + pb * BUFB;
+#pragma unroll
+      for (int q = 0; q < ROUNDS; ++q) {
+        const int idx = tid + kBlock * q;
+        const int r = idx / CPR;
+        const int ch = idx - r * CPR;
+        *reinterpret_cast<i32x4*>(b + r * ROWB + swz(r, ch) * 16) = pre[q];
+      }
+    }
   };
 
-  // One block: park the prefetched rows (register buffer pb) in LDS buffer
-  // pb, refill the register buffer with the block two ahead, MFMA, epilogue.
-  auto process = [&](int pb, int blk) {
-    unsigned char* b = smem + pb * BUF;
-#pragma unroll
-    for (int q = 0; q < ROUNDS; ++q) {
-      const int idx = tid + kBlock * q;
-      const int r = idx / CPR;
-      const int ch = idx - r * CPR;
-      *reinterpret_cast<i32x4*>(b + r * PITCH + ch * 16) = pre[pb][q];
-    }
+  const int blk0 = blockIdx.x;
+  issue_block(0, blk0);
+  int pb = 0;
+  // Blocks blk0 + j*G alternate between LDS buffers 0 and 1.  Buffer pb^1 is
+  // refilled (issue_block) right after the barrier of block j, which every
+  // wave passes only after finishing block j-1, the buffer's previous reader.
+  for (int blk = blk0; blk < p.nblocks; blk += gridDim.x) {
+    park_block(pb);
     if (wave == 0) {
-      const uint64_t bits = __ballot(pre_mask[pb] != 0u);
-      if (lane == 0) *reinterpret_cast<uint32_t*>(b + 32 * PITCH) = (uint32_t)bits;
+      const uint64_t bits = __ballot(pre_mask != 0u);
+      if (lane == 0) smask[pb] = (uint32_t)bits;
     }
+    __builtin_amdgcn_s_waitcnt(0);  // this block's copies into LDS have landed
     __syncthreads();
-    load_block(pb, blk + 2 * (int)gridDim.x);
-    f32x16 acc[TILES];
-#pragma unroll
-    for (int t = 0; t < TILES; ++t) acc[t] = f32x16{};
-    const unsigned char* arow = b + rl * PITCH + slot * 16;
+    issue_block(pb ^ 1, blk + gridDim.x);
+    const unsigned char* b = smem + pb * BUFB;
+    f32x16 acc = f32x16{};
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
-      const i32x4 a = *reinterpret_cast<const i32x4*>(arow + u * 32);
-#pragma unroll
-      for (int t = 0; t < TILES; ++t) Mfma<T>::unit(a, w[t][u], acc[t]);
+      const i32x4 a = *reinterpret_cast<const i32x4*>(b + rl * ROWB + swz(rl, 2 * u + slot) * 16);
+      Mfma<T>::unit(a, w[u], acc);
     }
-    const uint32_t mword = *reinterpret_cast<const uint32_t*>(b + 32 * PITCH);
+    const uint32_t mword = smask[pb];
     const int r0 = blk * 32;
     const bool odd = rl & 1;
+    const int cp = c_lane - (odd ? 1 : 0);  // first column of this lane's pair
+    const bool hi = SPLITN && cp >= p.nsplit;
+    const int cc = hi ? cp - p.nsplit : cp;
+    const uint32_t ldy = (uint32_t)(hi ? p.ldy1 : p.ldy0);
 #pragma unroll
-    for (int t = 0; t < TILES; ++t) {
-      const int c = col0 + 32 * t + rl;
-      const int cp = c - (odd ? 1 : 0);  // first column of this lane's pair
-      const bool hi = SPLITN && cp >= p.nsplit;
-      const int cc = hi ? cp - p.nsplit : cp;
-      const uint32_t ldy = (uint32_t)(hi ? p.ldy1 : p.ldy0);
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int i0 = 2 * jj, i1 = 2 * jj + 1;
-        const int ra = acc_row(i0, slot), rb = acc_row(i1, slot);
-        const float v0 = ((mword >> ra) & 1u) ? 0.f : acc[t][i0] + bias[t];
-        const float v1 = ((mword >> rb) & 1u) ? 0.f : acc[t][i1] + bias[t];
-        // even lane keeps row ra and takes the partner's (row ra, c+1);
-        // odd lane keeps row rb and takes the partner's (row rb, c-1).
-        const float x = swap_pair_lane(odd ? v0 : v1);
-        const int rr = odd ? rb : ra;
+    for (int jj = 0; jj < 8; ++jj) {
+      const int i0 = 2 * jj, i1 = 2 * jj + 1;
+      const int ra = acc_row(i0, slot), rb = acc_row(i1, slot);
+      const float v0 = ((mword >> ra) & 1u) ? 0.f : acc[i0] + bias;
+      const float v1 = ((mword >> rb) & 1u) ? 0.f : acc[i1] + bias;
+      // even lane keeps row ra and takes the partner's (row ra, c+1);
+      // odd lane keeps row rb and takes the partner's (row rb, c-1).
+      const float x = swap_pair_lane(odd ? v0 : v1);
+      const int rr = odd ? rb : ra;
+      PairT<T> pv = odd ? make_pair<T>(x, v1) : make_pair<T>(v0, x);
+      if constexpr (WIDE) {
+        *reinterpret_cast<PairT<T>*>(&sout[pb][rr * OPITCH + (cp - colw) * E]) = pv;
+      } else {
         const int row = r0 + rr;
-        PairT<T> pv = odd ? make_pair<T>(x, v1) : make_pair<T>(v0, x);
-        const uint32_t off = (row < nrows && cp < p.N)
-                                 ? ((uint32_t)row * ldy + (uint32_t)cc) * E
-                                 : kOob;
+        const uint32_t off =
+            (row < nrows && cp < p.N) ? ((uint32_t)row * ldy + (uint32_t)cc) * E : kOob;
         if constexpr (ACC) {
           const i32x2 old = __builtin_amdgcn_raw_buffer_load_b64(ry0, off, 0, 0);
           pv.x = __float_as_uint(__uint_as_float(pv.x) + __int_as_float(old[0]));
@@ -251,21 +337,31 @@ void proj_kernel(ProjArgs p) {
         }
       }
     }
-  };
-
-  const int blk0 = blockIdx.x;
-  load_block(0, blk0);
-  load_block(1, blk0 + gridDim.x);
-  // Weights, bias and the first blocks in one round trip; the loop then has
-  // only its own prefetch in flight.
-  __builtin_amdgcn_s_waitcnt(0);
-  // Blocks blk0 + j*G alternate between buffers 0 and 1 (a block past the end
-  // reads zeros and stores nothing).  LDS buffer pb is rewritten two blocks
-  // after it was read, behind the barrier of the block in between, which
-  // every wave reaches only after finishing that read.
-  for (int blk = blk0; blk < p.nblocks; blk += 2 * gridDim.x) {
-    process(0, blk);
-    process(1, blk + gridDim.x);
+    if constexpr (WIDE) {
+      // sout[pb] is rewritten two blocks later, behind the barrier of the
+      // block in between (see above), so one barrier here suffices.
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 32 * 16 / kBlock; ++i) {
+        const int id = tid + kBlock * i;
+        const int rr = id >> 4, ch = id & 15;
+        const int col = colw + ch * 8;
+        const int row = r0 + rr;
+        const bool h2 = SPLITN && col >= p.nsplit;
+        const uint32_t ld2 = (uint32_t)(h2 ? p.ldy1 : p.ldy0);
+        const int c2 = h2 ? col - p.nsplit : col;
+        const uint32_t off =
+            (row < nrows && col < p.N) ? ((uint32_t)row * ld2 + (uint32_t)c2) * E : kOob;
+        const i32x4 v = *reinterpret_cast<const i32x4*>(&sout[pb][rr * OPITCH + ch * 16]);
+        if constexpr (SPLITN) {
+          __builtin_amdgcn_raw_buffer_store_b128(v, ry0, h2 ? kOob : off, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(v, ry1, h2 ? off : kOob, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b128(v, ry0, off, 0, 0);
+        }
+      }
+    }
+    pb ^= 1;
   }
 }
 
@@ -314,7 +410,7 @@ __global__ __launch_bounds__(kBlock) void transpose_kernel(const void* w0, const
 // (dispatch is round-robin over the 8 XCDs): the re-reads of each G and X
 // row segment by the chunk's other tiles then hit the same L2.
 // ---------------------------------------------------------------------------
-template <class T, bool MASKED>
+template <class T, bool MASKED, bool SPLITG>
 __global__ __launch_bounds__(kBlock) void wgrad_kernel(WgradArgs p) {
   constexpr int E = T::kBytes;
   constexpr int EPU = 16 / E;
@@ -343,63 +439,91 @@ __global__ __launch_bounds__(kBlock) void wgrad_kernel(WgradArgs p) {
   const int64_t rbeg = (int64_t)chunk * p.rows_per_chunk;
   const int64_t rend = rbeg + p.rows_per_chunk < p.rows ? rbeg + p.rows_per_chunk : p.rows;
 
-  // This lane's two columns of the G and X tiles.
-  const int gc0 = n0 + 2 * lane, xc0 = k0 + 2 * lane;
-  const bool g_ok = gc0 < p.N, x_ok = xc0 < p.K;
-  const int gc = g_ok ? gc0 : 0, xc = x_ok ? xc0 : 0;  // dead lanes read column 0
+  // This lane's two columns of the G and X tiles, read through buffer
+  // descriptors based at the chunk's first row: the row offset is a
+  // wave-uniform scalar (soffset), the column a per-lane constant (voffset),
+  // and rows past the chunk's end fall outside num_records and read as zero.
+  const int gc = n0 + 2 * lane, xc = k0 + 2 * lane;
   const bool g_hi = gc >= p.nsplit;
-  const char* gbase = g_hi ? static_cast<const char*>(p.g1) + (int64_t)(gc - p.nsplit) * E
-                           : static_cast<const char*>(p.g0) + (int64_t)gc * E;
-  const int64_t ldg = g_hi ? p.ldg1 : p.ldg0;
-  const char* xbase = static_cast<const char*>(p.x) + (int64_t)xc * E;
+  const uint32_t ldg0 = (uint32_t)p.ldg0 * E, ldg1 = (uint32_t)p.ldg1 * E;
+  const uint32_t ldx = (uint32_t)p.ldx * E;
+  const int64_t nr = rend > rbeg ? rend - rbeg : 0;
+  const __amdgpu_buffer_rsrc_t rg0 =
+      make_rsrc(static_cast<const char*>(p.g0) + rbeg * p.ldg0 * E, (uint32_t)(nr * ldg0));
+  const __amdgpu_buffer_rsrc_t rg1 =
+      make_rsrc(SPLITG ? static_cast<const char*>(p.g1) + rbeg * p.ldg1 * E : p.g0,
+                SPLITG ? (uint32_t)(nr * ldg1) : 0u);
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(static_cast<const char*>(p.x) + rbeg * p.ldx * E, (uint32_t)(nr * ldx));
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc(MASKED ? p.mask + rbeg : p.x, MASKED ? (uint32_t)nr : 0u);
+  const uint32_t vg0 = (gc < p.N && !g_hi) ? (uint32_t)gc * E : kOob;
+  const uint32_t vg1 = (gc < p.N && g_hi) ? (uint32_t)(gc - p.nsplit) * E : kOob;
+  const uint32_t vx = xc < p.K ? (uint32_t)xc * E : kOob;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
 
-  // Loads are unconditional (rows clamped into the chunk, so every address is
-  // valid) and rows past the end or masked are zeroed when parked: the
-  // instruction stream is the same every step and the compiler's wait counts
-  // stay exact, so the next step's loads overlap this step's MFMAs.
-  Pair gp[RW], xp[RW];
-  uint32_t mk[RW];      // mask bytes, looked at only when parked
-  uint32_t inrange = 0; // bit i: row i of this wave's share exists
-  auto load_step = [&](int64_t r0) {
-    inrange = 0;
-#pragma unroll
-    for (int i = 0; i < RW; ++i) {
-      const int64_t row = r0 + wave * RW + i;
-      const int64_t rc = row < rend ? row : rend - 1;
-      gp[i] = *reinterpret_cast<const Pair*>(gbase + rc * ldg * E);
-      xp[i] = *reinterpret_cast<const Pair*>(xbase + rc * p.ldx * E);
-      if constexpr (MASKED) mk[i] = p.mask[rc];
-      inrange |= (row < rend ? 1u : 0u) << i;
+  // Four steps in flight (about 128 KB per workgroup): register sets 0..3
+  // rotate.  Masked rows are zeroed when parked: lane i < RW of a wave loads
+  // the mask byte of its share's row i, and a ballot turns them into bits.
+  constexpr int NSET = 4;
+  Pair gp[NSET][RW], xp[NSET][RW];
+  uint32_t mk[NSET];
+  auto ldpair = [](__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    if constexpr (E == 4) {
+      const i32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
+      return Pair{(uint32_t)v[0], (uint32_t)v[1]};
+    } else {
+      return (Pair)__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0);
     }
   };
-  auto park_step = [&](unsigned char* b) {
-    unsigned char* tg = b + (2 * lane) * PITCH + wave * RW * E;
-    unsigned char* tx = tg + TILE_BYTES;
+  auto load_step = [&](int sset, int64_t r0) {
+    const uint32_t row0 = (uint32_t)(r0 - rbeg) + (uint32_t)(wv * RW);
 #pragma unroll
     for (int i = 0; i < RW; ++i) {
-      bool live = (inrange >> i) & 1u;
-      if constexpr (MASKED) live = live && mk[i] == 0u;
-      if (!g_ok || !live) gp[i] = Pair{};
-      if (!x_ok || !live) xp[i] = Pair{};
+      Pair g = ldpair(rg0, vg0, (row0 + i) * ldg0);
+      if constexpr (SPLITG) {
+        const Pair g1 = ldpair(rg1, vg1, (row0 + i) * ldg1);
+        if constexpr (E == 4) {
+          g = Pair{g.x | g1.x, g.y | g1.y};
+        } else {
+          g |= g1;
+        }
+      }
+      gp[sset][i] = g;
+      xp[sset][i] = ldpair(rx, vx, (row0 + i) * ldx);
+    }
+    if constexpr (MASKED) {
+      mk[sset] = __builtin_amdgcn_raw_buffer_load_b8(rm, lane < RW ? (uint32_t)lane : kOob, row0, 0);
+    }
+  };
+  auto park_step = [&](int sset, unsigned char* b) {
+    unsigned char* tg = b + (2 * lane) * PITCH + wave * RW * E;
+    unsigned char* tx = tg + TILE_BYTES;
+    Pair gq[RW], xq[RW];
+    uint32_t masked = 0;
+    if constexpr (MASKED) masked = (uint32_t)__ballot(lane < RW && mk[sset] != 0u);
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      gq[i] = ((masked >> i) & 1u) ? Pair{} : gp[sset][i];
+      xq[i] = ((masked >> i) & 1u) ? Pair{} : xp[sset][i];
     }
 #pragma unroll
     for (int g = 0; g < RW; g += GROUP) {
       uint2 lo_g, hi_g, lo_x, hi_x;
       if constexpr (E == 4) {
-        lo_g = uint2{gp[g].x, gp[g + 1].x};
-        hi_g = uint2{gp[g].y, gp[g + 1].y};
-        lo_x = uint2{xp[g].x, xp[g + 1].x};
-        hi_x = uint2{xp[g].y, xp[g + 1].y};
+        lo_g = uint2{gq[g].x, gq[g + 1].x};
+        hi_g = uint2{gq[g].y, gq[g + 1].y};
+        lo_x = uint2{xq[g].x, xq[g + 1].x};
+        hi_x = uint2{xq[g].y, xq[g + 1].y};
       } else {
         // [r0.lo16 | r1.lo16] = perm(r1, r0, 0x05040100); hi halves 0x07060302.
-        lo_g = uint2{__builtin_amdgcn_perm(gp[g + 1], gp[g], 0x05040100u),
-                     __builtin_amdgcn_perm(gp[g + 3], gp[g + 2], 0x05040100u)};
-        hi_g = uint2{__builtin_amdgcn_perm(gp[g + 1], gp[g], 0x07060302u),
-                     __builtin_amdgcn_perm(gp[g + 3], gp[g + 2], 0x07060302u)};
-        lo_x = uint2{__builtin_amdgcn_perm(xp[g + 1], xp[g], 0x05040100u),
-                     __builtin_amdgcn_perm(xp[g + 3], xp[g + 2], 0x05040100u)};
-        hi_x = uint2{__builtin_amdgcn_perm(xp[g + 1], xp[g], 0x07060302u),
-                     __builtin_amdgcn_perm(xp[g + 3], xp[g + 2], 0x07060302u)};
+        lo_g = uint2{__builtin_amdgcn_perm(gq[g + 1], gq[g], 0x05040100u),
+                     __builtin_amdgcn_perm(gq[g + 3], gq[g + 2], 0x05040100u)};
+        hi_g = uint2{__builtin_amdgcn_perm(gq[g + 1], gq[g], 0x07060302u),
+                     __builtin_amdgcn_perm(gq[g + 3], gq[g + 2], 0x07060302u)};
+        lo_x = uint2{__builtin_amdgcn_perm(xq[g + 1], xq[g], 0x05040100u),
+                     __builtin_amdgcn_perm(xq[g + 3], xq[g + 2], 0x05040100u)};
+        hi_x = uint2{__builtin_amdgcn_perm(xq[g + 1], xq[g], 0x07060302u),
+                     __builtin_amdgcn_perm(xq[g + 3], xq[g + 2], 0x07060302u)};
       }
       *reinterpret_cast<uint2*>(tg + g * E) = lo_g;
       *reinterpret_cast<uint2*>(tg + PITCH + g * E) = hi_g;
@@ -421,13 +545,15 @@ __global__ __launch_bounds__(kBlock) void wgrad_kernel(WgradArgs p) {
     for (int c = 0; c < 2; ++c) acc[a][c] = f32x16{};
   }
   float bsum[2] = {0.f, 0.f};
-  int buf = 0;
-  if (rbeg < rend) load_step(rbeg);
-  for (int64_t r0 = rbeg; r0 < rend; r0 += RS) {
-    unsigned char* b = lds[buf];
-    park_step(b);
+  // One step: park register set `sset` in LDS buffer sset & 1, refill the set
+  // with the rows NSET steps ahead, MFMA.  An LDS buffer is rewritten two
+  // steps after it was read, behind the barrier of the step in between, which
+  // every wave passes only after finishing its reads.
+  auto step = [&](int sset, int64_t r0) {
+    unsigned char* b = lds[sset & 1];
+    park_step(sset, b);
     __syncthreads();
-    if (r0 + RS < rend) load_step(r0 + RS);
+    load_step(sset, r0 + NSET * RS);
     const unsigned char* ta = b + (wn * 64 + rl) * PITCH + slot * 16;
     const unsigned char* tb = b + TILE_BYTES + (wk * 64 + rl) * PITCH + slot * 16;
 #pragma unroll
@@ -459,7 +585,15 @@ __global__ __launch_bounds__(kBlock) void wgrad_kernel(WgradArgs p) {
         }
       }
     }
-    buf ^= 1;
+  };
+  if (rbeg < rend) {
+#pragma unroll
+    for (int s2 = 0; s2 < NSET; ++s2) load_step(s2, rbeg + s2 * RS);
+    // Steps past the end read zeros (outside the descriptors): harmless.
+    for (int64_t r0 = rbeg; r0 < rend; r0 += NSET * RS) {
+#pragma unroll
+      for (int s2 = 0; s2 < NSET; ++s2) step(s2, r0 + s2 * RS);
+    }
   }
 
   // ---- partials out (plain stores; every slot of ws is written) ----
@@ -486,42 +620,85 @@ __global__ __launch_bounds__(kBlock) void wgrad_kernel(WgradArgs p) {
   }
 }
 
-// dW / db = fixed-order sums of the chunk partials, rounded once.
+// dW / db = fixed-order sums of the chunk partials, rounded once.  A
+// workgroup owns 64 consecutive outputs (16 groups of 4) and all chunks: lane
+// t loads outputs 4*(t%16).. of chunks t/16, t/16 + 16, ... (16-byte loads,
+// all issued together), sums them in chunk order, and a fixed LDS tree adds
+// the 16 chunk residues -- the same order on every run.
 template <class T>
 __global__ __launch_bounds__(kBlock) void wgrad_reduce_kernel(WgradArgs p, void* dw0, void* dw1,
                                                               void* db0, void* db1) {
+  __shared__ float4 red[kBlock];
   const int64_t nk = (int64_t)p.N * p.K;
   const int64_t total = nk + (p.wsb != nullptr ? p.N : 0);
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * kBlock) {
-    float s = 0.f;
-    if (i < nk) {
-      // Fixed order c = 0, 1, ...; eight loads in flight at a time.
-      int c = 0;
-      for (; c + 8 <= p.nchunks; c += 8) {
-        float v[8];
+  const int g = threadIdx.x & 15, cs = threadIdx.x >> 4;
+  const int nper = (p.nchunks + 15) / 16;  // chunks per lane (some past the end)
+  for (int64_t base = (int64_t)blockIdx.x * 64; base < total; base += (int64_t)gridDim.x * 64) {
+    const int64_t i0 = base + 4 * g;  // this lane's 4 outputs: i0 .. i0+3
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (base + 64 <= nk && (nk & 3) == 0) {
+      for (int j0 = 0; j0 < nper; j0 += 4) {
+        float4 v[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = p.ws[(int64_t)(c + u) * nk + i];
+        for (int jj = 0; jj < 4; ++jj) {
+          const int c = cs + 16 * (j0 + jj);
+          const int cc = c < p.nchunks ? c : p.nchunks - 1;
+          v[jj] = *reinterpret_cast<const float4*>(p.ws + (int64_t)cc * nk + i0);
+          if (c >= p.nchunks) v[jj] = float4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) s += v[u];
-      }
-      for (; c < p.nchunks; ++c) s += p.ws[(int64_t)c * nk + i];
-      const int n = (int)(i / p.K);
-      const int k = (int)(i - (int64_t)n * p.K);
-      if (n < p.nsplit) {
-        if (dw0 != nullptr) store1<T>(dw0, (uint64_t)n * p.K + k, s);
-      } else if (dw1 != nullptr) {
-        store1<T>(dw1, (uint64_t)(n - p.nsplit) * p.K + k, s);
+        for (int jj = 0; jj < 4; ++jj) {
+          acc.x += v[jj].x; acc.y += v[jj].y; acc.z += v[jj].z; acc.w += v[jj].w;
+        }
       }
     } else {
-      const int n = (int)(i - nk);
-      for (int c = 0; c < p.nchunks; ++c) s += p.wsb[(int64_t)c * p.N + n];
-      if (n < p.nsplit) {
-        if (db0 != nullptr) store1<T>(db0, (uint64_t)n, s);
-      } else if (db1 != nullptr) {
-        store1<T>(db1, (uint64_t)(n - p.nsplit), s);
+      float t[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int e = 0; e < 4; ++e) {
+        const int64_t i = i0 + e;
+        if (i >= total) continue;
+        for (int c = cs; c < p.nchunks; c += 16) {
+          t[e] += i < nk ? p.ws[(int64_t)c * nk + i] : p.wsb[(int64_t)c * p.N + (i - nk)];
+        }
+      }
+      acc = float4{t[0], t[1], t[2], t[3]};
+    }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+#pragma unroll
+    for (int h = 8; h >= 1; h >>= 1) {  // chunk groups cs, cs + h
+      if (cs < h) {
+        float4 o = red[threadIdx.x + 16 * h];
+        float4 m = red[threadIdx.x];
+        m.x += o.x; m.y += o.y; m.z += o.z; m.w += o.w;
+        red[threadIdx.x] = m;
+      }
+      __syncthreads();
+    }
+    if (cs == 0) {
+      const float sv[4] = {red[g].x, red[g].y, red[g].z, red[g].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t i = i0 + e;
+        if (i >= total) continue;
+        if (i < nk) {
+          const int n = (int)(i / p.K);
+          const int k = (int)(i - (int64_t)n * p.K);
+          if (n < p.nsplit) {
+            if (dw0 != nullptr) store1<T>(dw0, (uint64_t)n * p.K + k, sv[e]);
+          } else if (dw1 != nullptr) {
+            store1<T>(dw1, (uint64_t)(n - p.nsplit) * p.K + k, sv[e]);
+          }
+        } else {
+          const int n = (int)(i - nk);
+          if (n < p.nsplit) {
+            if (db0 != nullptr) store1<T>(db0, (uint64_t)n, sv[e]);
+          } else if (db1 != nullptr) {
+            store1<T>(db1, (uint64_t)(n - p.nsplit), sv[e]);
+          }
+        }
       }
     }
+    __syncthreads();
   }
 }
 
@@ -540,37 +717,37 @@ int cu_count() {
   return cached[dev];
 }
 
-template <class T, int TILES, bool ACC, bool SPLITA, bool SPLITN>
+template <class T, int NU, bool ACC, bool SPLITA, bool SPLITN>
 hipError_t launch_proj_t(ProjArgs a, hipStream_t st) {
-  const int cols_per_wg = 4 * 32 * TILES;
-  const int gy = (a.N + cols_per_wg - 1) / cols_per_wg;
-  // One resident workgroup per CU (the weight registers take a whole SIMD
-  // slot per wave); blocks split evenly over grid.x.
-  int want = cu_count() / gy;
-  if (want < 1) want = 1;
+  const int gy = (a.N + 127) / 128;
+  // Resident workgroups per CU = waves per SIMD (4 waves per workgroup).
+  const int occ = proj_waves_per_eu<NU, SPLITA>();
+  int want = cu_count() * occ / gy;
+  want = (want + 7) / 8 * 8;  // keep gx a multiple of 8: same XCD across grid.y
   const int per = (a.nblocks + want - 1) / want;
-  const int gx = (a.nblocks + per - 1) / per;
-  hipLaunchKernelGGL((proj_kernel<T, TILES, ACC, SPLITA, SPLITN>), dim3(gx, gy), dim3(kBlock), 0,
-                     st, a);
+  int gx = (a.nblocks + per - 1) / per;
+  gx = (gx + 7) / 8 * 8;
+  hipLaunchKernelGGL((proj_kernel<T, NU, ACC, SPLITA, SPLITN>), dim3(gx, gy), dim3(kBlock), 0, st,
+                     a);
   return hipGetLastError();
 }
 
-template <class T, int TILES, bool ACC>
+template <class T, int NU, bool ACC>
 hipError_t launch_proj_split(const ProjArgs& a, hipStream_t st) {
   const bool sa = a.ksplit < a.K, sn = a.nsplit < a.N;
-  if (sa) return launch_proj_t<T, TILES, ACC, true, false>(a, st);  // never both: callers
-  if (sn) return launch_proj_t<T, TILES, ACC, false, true>(a, st);  // split one side only
-  return launch_proj_t<T, TILES, ACC, false, false>(a, st);
+  if (sa) return launch_proj_t<T, NU, ACC, true, false>(a, st);  // never both: callers
+  if (sn) return launch_proj_t<T, NU, ACC, false, true>(a, st);  // split one side only
+  return launch_proj_t<T, NU, ACC, false, false>(a, st);
 }
 
 template <class T>
 hipError_t launch_proj_dtype(const ProjArgs& a, bool accumulate, hipStream_t st) {
   if constexpr (T::kBytes == 4) {
-    if (accumulate) return launch_proj_split<T, 1, true>(a, st);
-    return launch_proj_split<T, 1, false>(a, st);
+    if (accumulate) return launch_proj_split<T, 32, true>(a, st);
+    return launch_proj_split<T, 32, false>(a, st);
   } else {
-    if (a.K <= 256) return launch_proj_split<T, 2, false>(a, st);
-    return launch_proj_split<T, 1, false>(a, st);
+    if (a.K <= 256) return launch_proj_split<T, 16, false>(a, st);
+    return launch_proj_split<T, 32, false>(a, st);
   }
 }
 
@@ -578,16 +755,21 @@ template <class T>
 hipError_t launch_wgrad_t(WgradArgs a, void* dw0, void* dw1, void* db0, void* db1,
                           hipStream_t st) {
   const int nblk = a.nchunks * a.ntile_n * a.ntile_k;
-  if (a.mask != nullptr) {
-    hipLaunchKernelGGL((wgrad_kernel<T, true>), dim3(nblk), dim3(kBlock), 0, st, a);
+  const bool m = a.mask != nullptr, sg = a.nsplit < a.N;
+  if (m && sg) {
+    hipLaunchKernelGGL((wgrad_kernel<T, true, true>), dim3(nblk), dim3(kBlock), 0, st, a);
+  } else if (m) {
+    hipLaunchKernelGGL((wgrad_kernel<T, true, false>), dim3(nblk), dim3(kBlock), 0, st, a);
+  } else if (sg) {
+    hipLaunchKernelGGL((wgrad_kernel<T, false, true>), dim3(nblk), dim3(kBlock), 0, st, a);
   } else {
-    hipLaunchKernelGGL((wgrad_kernel<T, false>), dim3(nblk), dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL((wgrad_kernel<T, false, false>), dim3(nblk), dim3(kBlock), 0, st, a);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t total = (int64_t)a.N * a.K + a.N;
-  int64_t g = (total + kBlock - 1) / kBlock;
-  if (g > 2048) g = 2048;
+  int64_t g = (total + 63) / 64;
+  if (g > 4096) g = 4096;
   hipLaunchKernelGGL(wgrad_reduce_kernel<T>, dim3((int)g), dim3(kBlock), 0, st, a, dw0, dw1,
                      db0, db1);
   return hipGetLastError();
@@ -664,6 +846,11 @@ void wgrad_plan(int64_t rows, int n, int k, int dtype, WgradArgs* a) {
   int64_t steps = (rows + rs - 1) / rs;
   if (steps < 1) steps = 1;
   int64_t per = (steps + want - 1) / want;  // steps per chunk
+  per = (per + 3) / 4 * 4;                   // the kernel runs steps in fours
+  // Buffer descriptors cover one chunk: keep its rows under 2^31 bytes.
+  const int64_t row_bytes = (int64_t)(n > k ? n : k) * (dtype == kF32 ? 4 : 2);
+  const int64_t max_steps = (((int64_t)1 << 31) - 1) / (row_bytes * rs) / 4 * 4;
+  if (per > max_steps) per = max_steps > 4 ? max_steps : 4;
   int64_t chunks = (steps + per - 1) / per;
   chunks = (chunks + 7) / 8 * 8;
   a->rows_per_chunk = per * rs;
