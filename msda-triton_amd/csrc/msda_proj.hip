@@ -420,8 +420,6 @@ __global__ __launch_bounds__(kBlock) void wgrad_kernel(WgradArgs p) {
   constexpr int RW = RS / 4;           // rows per wave per step
   constexpr int PITCH = RS * E + 8;    // LDS bytes per transposed column
   constexpr int TILE_BYTES = TW * PITCH;
-  constexpr int GROUP = 8 / E;         // rows per 8-byte LDS piece
-  using Pair = typename std::conditional<E == 4, uint2, uint32_t>::type;
   __shared__ __align__(16) unsigned char lds[2][2 * TILE_BYTES];
 
   const int tid = threadIdx.x;
@@ -439,11 +437,19 @@ __global__ __launch_bounds__(kBlock) void wgrad_kernel(WgradArgs p) {
   const int64_t rbeg = (int64_t)chunk * p.rows_per_chunk;
   const int64_t rend = rbeg + p.rows_per_chunk < p.rows ? rbeg + p.rows_per_chunk : p.rows;
 
-  // This lane's two columns of the G and X tiles, read through buffer
-  // descriptors based at the chunk's first row: the row offset is a
-  // wave-uniform scalar (soffset), the column a per-lane constant (voffset),
-  // and rows past the chunk's end fall outside num_records and read as zero.
-  const int gc = n0 + 2 * lane, xc = k0 + 2 * lane;
+  // Staging: lane l covers CPL = 16/E consecutive columns (one 16-byte load)
+  // of RG row groups; each group is NI = 4 consecutive rows, so one wave
+  // instruction reads RG rows x 256 bytes (coalesced) and a lane ends up with a
+  // 4-row x CPL-column block that it writes to LDS column by column.  G and X
+  // are read through buffer descriptors based at the chunk's first row: the
+  // row offset is a wave-uniform scalar (soffset), the lane's row group and
+  // columns a per-lane constant (voffset), and rows past the chunk's end fall
+  // outside num_records and read as zero.
+  constexpr int CPL = 16 / E;      // columns per lane
+  constexpr int LPR = TW / CPL;    // lanes per tile row
+  constexpr int NI = 4;            // rows per group (loads per tensor per step)
+  const int lc = lane % LPR, rg = lane / LPR;
+  const int gc = n0 + lc * CPL, xc = k0 + lc * CPL;
   const bool g_hi = gc >= p.nsplit;
   const uint32_t ldg0 = (uint32_t)p.ldg0 * E, ldg1 = (uint32_t)p.ldg1 * E;
   const uint32_t ldx = (uint32_t)p.ldx * E;
@@ -456,79 +462,77 @@ __global__ __launch_bounds__(kBlock) void wgrad_kernel(WgradArgs p) {
   const __amdgpu_buffer_rsrc_t rx =
       make_rsrc(static_cast<const char*>(p.x) + rbeg * p.ldx * E, (uint32_t)(nr * ldx));
   const __amdgpu_buffer_rsrc_t rm = make_rsrc(MASKED ? p.mask + rbeg : p.x, MASKED ? (uint32_t)nr : 0u);
-  const uint32_t vg0 = (gc < p.N && !g_hi) ? (uint32_t)gc * E : kOob;
-  const uint32_t vg1 = (gc < p.N && g_hi) ? (uint32_t)(gc - p.nsplit) * E : kOob;
-  const uint32_t vx = xc < p.K ? (uint32_t)xc * E : kOob;
+  const uint32_t rgo = (uint32_t)(rg * NI);
+  const uint32_t vg0 = (gc < p.N && !g_hi) ? rgo * ldg0 + (uint32_t)gc * E : kOob;
+  const uint32_t vg1 = (gc < p.N && g_hi) ? rgo * ldg1 + (uint32_t)(gc - p.nsplit) * E : kOob;
+  const uint32_t vx = xc < p.K ? rgo * ldx + (uint32_t)xc * E : kOob;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
 
   // Four steps in flight (about 128 KB per workgroup): register sets 0..3
   // rotate.  Masked rows are zeroed when parked: lane i < RW of a wave loads
   // the mask byte of its share's row i, and a ballot turns them into bits.
   constexpr int NSET = 4;
-  Pair gp[NSET][RW], xp[NSET][RW];
+  i32x4 gp[NSET][NI], xp[NSET][NI];
   uint32_t mk[NSET];
-  auto ldpair = [](__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
-    if constexpr (E == 4) {
-      const i32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
-      return Pair{(uint32_t)v[0], (uint32_t)v[1]};
-    } else {
-      return (Pair)__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0);
-    }
-  };
   auto load_step = [&](int sset, int64_t r0) {
     const uint32_t row0 = (uint32_t)(r0 - rbeg) + (uint32_t)(wv * RW);
 #pragma unroll
-    for (int i = 0; i < RW; ++i) {
-      Pair g = ldpair(rg0, vg0, (row0 + i) * ldg0);
-      if constexpr (SPLITG) {
-        const Pair g1 = ldpair(rg1, vg1, (row0 + i) * ldg1);
-        if constexpr (E == 4) {
-          g = Pair{g.x | g1.x, g.y | g1.y};
-        } else {
-          g |= g1;
-        }
-      }
+    for (int i = 0; i < NI; ++i) {
+      i32x4 g = __builtin_amdgcn_raw_buffer_load_b128(rg0, vg0, (row0 + i) * ldg0, 0);
+      if constexpr (SPLITG) g |= __builtin_amdgcn_raw_buffer_load_b128(rg1, vg1, (row0 + i) * ldg1, 0);
       gp[sset][i] = g;
-      xp[sset][i] = ldpair(rx, vx, (row0 + i) * ldx);
+      xp[sset][i] = __builtin_amdgcn_raw_buffer_load_b128(rx, vx, (row0 + i) * ldx, 0);
     }
     if constexpr (MASKED) {
       mk[sset] = __builtin_amdgcn_raw_buffer_load_b8(rm, lane < RW ? (uint32_t)lane : kOob, row0, 0);
     }
   };
   auto park_step = [&](int sset, unsigned char* b) {
-    unsigned char* tg = b + (2 * lane) * PITCH + wave * RW * E;
-    unsigned char* tx = tg + TILE_BYTES;
-    Pair gq[RW], xq[RW];
     uint32_t masked = 0;
-    if constexpr (MASKED) masked = (uint32_t)__ballot(lane < RW && mk[sset] != 0u);
+    if constexpr (MASKED) masked = (uint32_t)__ballot(lane < RW && mk[sset] != 0u) >> rgo;
+    i32x4 gq[NI], xq[NI];
 #pragma unroll
-    for (int i = 0; i < RW; ++i) {
-      gq[i] = ((masked >> i) & 1u) ? Pair{} : gp[sset][i];
-      xq[i] = ((masked >> i) & 1u) ? Pair{} : xp[sset][i];
+    for (int i = 0; i < NI; ++i) {
+      const bool off = (masked >> i) & 1u;
+      gq[i] = off ? i32x4{0, 0, 0, 0} : gp[sset][i];
+      xq[i] = off ? i32x4{0, 0, 0, 0} : xp[sset][i];
     }
+    // Tile column c lives in LDS row c ^ ((c >> 5) & 3) (see cslot): the
+    // writers of one instruction (columns 8*lc + j, or 4*lc + j for fp32)
+    // then hit distinct bank groups, and the 32 consecutive columns a
+    // fragment read covers stay a permutation of 32 rows.  Row span of this
+    // lane: wave*RW + rgo + 0..3.
+    unsigned char* rowoff = b + (wave * RW + (int)rgo) * E;
+    const int a = (lc * CPL >> 5) & 3;
+    auto col = [&](int j) { return rowoff + (lc * CPL + (j ^ a)) * PITCH; };
+    if constexpr (E == 4) {
 #pragma unroll
-    for (int g = 0; g < RW; g += GROUP) {
-      uint2 lo_g, hi_g, lo_x, hi_x;
-      if constexpr (E == 4) {
-        lo_g = uint2{gq[g].x, gq[g + 1].x};
-        hi_g = uint2{gq[g].y, gq[g + 1].y};
-        lo_x = uint2{xq[g].x, xq[g + 1].x};
-        hi_x = uint2{xq[g].y, xq[g + 1].y};
-      } else {
-        // [r0.lo16 | r1.lo16] = perm(r1, r0, 0x05040100); hi halves 0x07060302.
-        lo_g = uint2{__builtin_amdgcn_perm(gq[g + 1], gq[g], 0x05040100u),
-                     __builtin_amdgcn_perm(gq[g + 3], gq[g + 2], 0x05040100u)};
-        hi_g = uint2{__builtin_amdgcn_perm(gq[g + 1], gq[g], 0x07060302u),
-                     __builtin_amdgcn_perm(gq[g + 3], gq[g + 2], 0x07060302u)};
-        lo_x = uint2{__builtin_amdgcn_perm(xq[g + 1], xq[g], 0x05040100u),
-                     __builtin_amdgcn_perm(xq[g + 3], xq[g + 2], 0x05040100u)};
-        hi_x = uint2{__builtin_amdgcn_perm(xq[g + 1], xq[g], 0x07060302u),
-                     __builtin_amdgcn_perm(xq[g + 3], xq[g + 2], 0x07060302u)};
+      for (int j = 0; j < 4; ++j) {
+        unsigned char* tg = col(j);
+        unsigned char* tx = tg + TILE_BYTES;
+        *reinterpret_cast<uint2*>(tg) = uint2{(uint32_t)gq[0][j], (uint32_t)gq[1][j]};
+        *reinterpret_cast<uint2*>(tg + 8) = uint2{(uint32_t)gq[2][j], (uint32_t)gq[3][j]};
+        *reinterpret_cast<uint2*>(tx) = uint2{(uint32_t)xq[0][j], (uint32_t)xq[1][j]};
+        *reinterpret_cast<uint2*>(tx + 8) = uint2{(uint32_t)xq[2][j], (uint32_t)xq[3][j]};
       }
-      *reinterpret_cast<uint2*>(tg + g * E) = lo_g;
-      *reinterpret_cast<uint2*>(tg + PITCH + g * E) = hi_g;
-      *reinterpret_cast<uint2*>(tx + g * E) = lo_x;
-      *reinterpret_cast<uint2*>(tx + PITCH + g * E) = hi_x;
+    } else {
+      // dword m of a row = columns 2m (low half) and 2m+1 (high half);
+      // [r0.lo16 | r1.lo16] = perm(r1, r0, 0x05040100), high halves 0x07060302.
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const uint32_t g0 = gq[0][m], g1 = gq[1][m], g2 = gq[2][m], g3 = gq[3][m];
+        const uint32_t x0 = xq[0][m], x1 = xq[1][m], x2 = xq[2][m], x3 = xq[3][m];
+        unsigned char* te = col(2 * m);
+        unsigned char* to = col(2 * m + 1);
+        *reinterpret_cast<uint2*>(te) =
+            uint2{__builtin_amdgcn_perm(g1, g0, 0x05040100u), __builtin_amdgcn_perm(g3, g2, 0x05040100u)};
+        *reinterpret_cast<uint2*>(to) =
+            uint2{__builtin_amdgcn_perm(g1, g0, 0x07060302u), __builtin_amdgcn_perm(g3, g2, 0x07060302u)};
+        *reinterpret_cast<uint2*>(te + TILE_BYTES) =
+            uint2{__builtin_amdgcn_perm(x1, x0, 0x05040100u), __builtin_amdgcn_perm(x3, x2, 0x05040100u)};
+        *reinterpret_cast<uint2*>(to + TILE_BYTES) =
+            uint2{__builtin_amdgcn_perm(x1, x0, 0x07060302u), __builtin_amdgcn_perm(x3, x2, 0x07060302u)};
+      }
     }
   };
   auto frag = [](const unsigned char* q) {
@@ -554,15 +558,22 @@ __global__ __launch_bounds__(kBlock) void wgrad_kernel(WgradArgs p) {
     park_step(sset, b);
     __syncthreads();
     load_step(sset, r0 + NSET * RS);
-    const unsigned char* ta = b + (wn * 64 + rl) * PITCH + slot * 16;
-    const unsigned char* tb = b + TILE_BYTES + (wk * 64 + rl) * PITCH + slot * 16;
+    // Fragment rows: column c = base + rl with base = 64*w + 32*h, stored in
+    // LDS row c ^ ((c >> 5) & 3) = base + (rl ^ ((2*w + h) & 3)).
+    const unsigned char* ta[2];
+    const unsigned char* tb[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      ta[h] = b + (wn * 64 + h * 32 + (rl ^ ((2 * wn + h) & 3))) * PITCH + slot * 16;
+      tb[h] = b + TILE_BYTES + (wk * 64 + h * 32 + (rl ^ ((2 * wk + h) & 3))) * PITCH + slot * 16;
+    }
 #pragma unroll
     for (int u = 0; u < RS / UK; ++u) {
       i32x4 fa[2], fb[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        fa[h] = frag(ta + h * 32 * PITCH + u * 32);
-        fb[h] = frag(tb + h * 32 * PITCH + u * 32);
+        fa[h] = frag(ta[h] + u * 32);
+        fb[h] = frag(tb[h] + u * 32);
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
