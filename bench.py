@@ -25,6 +25,9 @@ Prints ONE JSON line:
   fused_front_end  decoder shapes: the fused MSDeformAttn front-end (softmax,
                reference point + offset in the kernels) vs the same front-end
                composed from PyTorch ops around the operator
+  projections  the attention layer's projections either side of the operator
+               (value / offset+logit / output) on the library's MFMA kernels vs
+               torch's linear (+ masked_fill) and its backward
   cpu_baseline the CPU oracle (grid_sample restatement) on the host cores
 """
 
@@ -303,6 +306,96 @@ def fused_front_end_times(lib, preset: str = "decoder") -> dict:
     return {k: (round(v, 2) if isinstance(v, float) else v) for k, v in res.items()}
 
 
+def projection_times(lib, preset: str = "decoder", pad_fraction: float = 0.1) -> dict:
+    """The attention layer's projections around the operator
+    (labs/solutions/lab00.py:199-208) at the preset's sizes: value_proj over
+    the B*S value rows (a `pad_fraction` of rows flagged as padding, zeroed
+    after the projection as Deformable-DETR does), the offset + logit
+    projections of the B*Q query rows (one split call), out_proj over the B*Q
+    operator outputs.  Ours: msda_projection_forward / _backward (grad of
+    input, weight and bias).  Torch: F.linear (+ masked_fill), and the
+    backward autograd runs for it (masked_fill of the gradient, grad_input,
+    grad_weight, grad_bias).  Graph-replayed device time per call."""
+    import torch
+
+    from msda_triton_amd import presets
+    from msda_triton_amd.ops import _DTYPE_CODE
+
+    dev = torch.device("cuda", 0)
+    c = presets.preset_dims(preset)
+    B, S, M, D, Q, L, K = c["B"], c["S"], c["M"], c["D"], c["Q"], c["L"], c["K"]
+    C = M * D
+    dtype = presets.make_preset_inputs(preset, device="cpu")[0].dtype
+    code = _DTYPE_CODE[dtype]
+    e = torch.empty((), dtype=dtype).element_size()
+    g = torch.Generator().manual_seed(3)
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def one(name, rows, n1, n2, masked):
+        x = torch.randn(rows, C, generator=g).to(dev, dtype)
+        w1 = (torch.randn(n1, C, generator=g) / C ** 0.5).to(dev, dtype)
+        b1 = torch.randn(n1, generator=g).to(dev, dtype)
+        w2 = (torch.randn(n2, C, generator=g) / C ** 0.5).to(dev, dtype) if n2 else None
+        b2 = torch.randn(n2, generator=g).to(dev, dtype) if n2 else None
+        mask = (torch.rand(rows, generator=g) < pad_fraction).to(dev) if masked else None
+        m8 = None if mask is None else mask.view(torch.uint8)
+        y1 = torch.empty(rows, n1, device=dev, dtype=dtype)
+        y2 = torch.empty(rows, n2, device=dev, dtype=dtype) if n2 else None
+        gy1 = torch.randn(rows, n1, generator=g).to(dev, dtype)
+        gy2 = torch.randn(rows, n2, generator=g).to(dev, dtype) if n2 else None
+        gx, gw1, gb1 = torch.empty_like(x), torch.empty_like(w1), torch.empty_like(b1)
+        gw2 = torch.empty_like(w2) if n2 else None
+        gb2 = torch.empty_like(b2) if n2 else None
+        N = n1 + n2
+        ws = torch.empty(lib.msda_projection_workspace_bytes(rows, C, N, code),
+                         dtype=torch.uint8, device=dev)
+
+        def ours_fwd():
+            assert lib.msda_projection_forward(p(x), p(w1), p(b1), p(w2), p(b2), p(m8), p(y1),
+                                               p(y2), rows, C, N, n1, code, st()) == 0
+
+        def ours_bwd():
+            assert lib.msda_projection_backward(p(x), p(w1), p(w2), p(m8), p(gy1), p(gy2), p(gx),
+                                                p(gw1), p(gb1), p(gw2), p(gb2), p(ws), rows, C, N,
+                                                n1, code, st()) == 0
+
+        def torch_fwd():
+            o = torch.nn.functional.linear(x, w1, b1)
+            if mask is not None:
+                o = o.masked_fill(mask[:, None], 0)
+            if n2:
+                torch.nn.functional.linear(x, w2, b2)
+
+        def torch_bwd():
+            gx_ = None
+            for gy, w in ((gy1, w1), (gy2, w2)):
+                if w is None:
+                    continue
+                gm = gy.masked_fill(mask[:, None], 0) if mask is not None else gy
+                gx_ = gm @ w if gx_ is None else gx_ + gm @ w
+                torch.mm(gm.t(), x)
+                gm.sum(0)
+
+        r = {"rows": rows, "in": C, "out": N, "masked": masked,
+             "fwd_us": _graph_us(ours_fwd, dev), "bwd_us": _graph_us(ours_bwd, dev),
+             "torch_fwd_us": _graph_us(torch_fwd, dev), "torch_bwd_us": _graph_us(torch_bwd, dev)}
+        # algorithmic bytes: fwd reads x and W, writes y; bwd reads x, W, dy
+        # and writes dx, dW, db
+        r["fwd_bytes"] = (rows * (C + N) + N * C + N) * e
+        r["bwd_bytes"] = (rows * (2 * C + N) + 2 * N * C + N) * e
+        r["fwd_GBps"] = r["fwd_bytes"] / r["fwd_us"] / 1e3
+        r["bwd_GBps"] = r["bwd_bytes"] / r["bwd_us"] / 1e3
+        return name, {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r.items()}
+
+    res = dict([one("value_proj", B * S, C, 0, True),
+                one("offset_weight_proj", B * Q, M * L * K * 2, M * L * K, False),
+                one("out_proj", B * Q, C, 0, False)])
+    tot = {k: round(sum(v[k] for v in res.values()), 2)
+           for k in ("fwd_us", "bwd_us", "torch_fwd_us", "torch_bwd_us")}
+    return {"preset": preset, "dtype": str(dtype).replace("torch.", ""), **res, "total": tot}
+
+
 OTHER_PRESETS = ("tiny", "encoder", "high_contention", "mask2former_fp32", "mask2former_bf16")
 
 
@@ -323,6 +416,8 @@ def main() -> int:
     ap.add_argument("--calls", choices=("operator", "fused", "deterministic"),
                     default="operator",
                     help="with --pmc-driver: which entry points the calls go through")
+    ap.add_argument("--projections-only", action="store_true",
+                    help="print only the projection timings (JSON) -- a short run to profile")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -342,6 +437,9 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     lib = _native.load()
+    if args.projections_only:
+        print(json.dumps({"projections": projection_times(lib, args.preset)}), flush=True)
+        return 0
 
     c = presets.preset_dims(args.preset)
     B, S, M, D, Q, L, K = c["B"], c["S"], c["M"], c["D"], c["Q"], c["L"], c["K"]
@@ -527,6 +625,7 @@ def main() -> int:
             for name in OTHER_PRESETS if name != args.preset
         }
         record["fused_front_end"] = fused_front_end_times(lib)
+        record["projections"] = projection_times(lib)
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline(args.preset)
     print(json.dumps(record), flush=True)
