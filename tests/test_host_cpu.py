@@ -244,3 +244,58 @@ def test_mmcv_shim_signature_and_validation():
     value, shapes, starts, loc, attn = _inputs()
     with pytest.raises(ValueError, match="CUDA"):
         MultiScaleDeformableAttnFunction.apply(value, shapes, starts, loc, attn, 64)
+
+
+# --- Projection entry points: argument checks before any launch ----------
+
+def call_proj_fwd(lib, **kw):
+    a = dict(x=16, w=16, b=None, w2=None, b2=None, m=None, y=16, y2=None, rows=4, cin=256, out=256,
+             split=256, dtype=2)
+    a.update(kw)
+    return lib.msda_projection_forward(a["x"], a["w"], a["b"], a["w2"], a["b2"], a["m"], a["y"],
+                                       a["y2"], a["rows"], a["cin"], a["out"], a["split"],
+                                       a["dtype"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=5), 2),
+    (dict(rows=-1), 1),
+    (dict(split=300), 1),            # split > out_features
+    (dict(split=0), 1),
+    (dict(cin=20), 3),               # 40-byte bf16 rows: not a multiple of 16 bytes
+    (dict(cin=520), 3),              # half-precision reduction longer than 512
+    (dict(split=128), 1),            # two outputs but no weight2 / output2
+    (dict(x=None), 1),
+    (dict(x=8), 3),                  # input pointer not 16-byte aligned
+    (dict(rows=0), 0),               # nothing to launch
+])
+def test_projection_forward_argument_errors(lib, kw, code):
+    assert call_proj_fwd(lib, **kw) == code
+
+
+def test_projection_backward_argument_errors(lib):
+    def bwd(**kw):
+        a = dict(x=16, w=16, w2=None, m=None, gy=16, gy2=None, gx=16, gw=None, gb=None, gw2=None,
+                 gb2=None, ws=16, rows=4, cin=256, out=256, split=256, dtype=2)
+        a.update(kw)
+        return lib.msda_projection_backward(a["x"], a["w"], a["w2"], a["m"], a["gy"], a["gy2"],
+                                            a["gx"], a["gw"], a["gb"], a["gw2"], a["gb2"], a["ws"],
+                                            a["rows"], a["cin"], a["out"], a["split"], a["dtype"],
+                                            None)
+    assert bwd(split=100) == 3        # split not a multiple of 8 bf16 elements
+    assert bwd(ws=None) == 1          # grad_input needs the workspace (transposed weight)
+    assert bwd(gy=None) == 1
+    assert bwd(out=600) == 3          # half grad_input reduction over 600 outputs
+    assert bwd(gy=24) == 3            # misaligned grad_output
+    assert bwd(rows=0, gx=None) == 0  # nothing requested, nothing launched
+    assert lib.msda_projection_workspace_bytes(100, 20, 256, 2) == -1
+    assert lib.msda_projection_workspace_bytes(100, 256, 256, 9) == -1
+
+
+def test_projection_rejects_cpu_tensors():
+    from msda_triton_amd.projection import projection
+
+    x = torch.randn(3, 16)
+    w = torch.randn(8, 16)
+    with pytest.raises(ValueError, match="CUDA"):
+        projection(x, w)
