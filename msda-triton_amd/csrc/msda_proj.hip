@@ -294,7 +294,11 @@ void proj_kernel(ProjArgs p) {
     __syncthreads();
     issue_block(pb ^ 1, blk + gridDim.x);
     const unsigned char* b = smem + pb * BUFB;
-    f32x16 acc = f32x16{};
+    // The accumulator starts at the bias (every element of a lane's tile is
+    // in its column), so the epilogue adds nothing.
+    f32x16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = bias;
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
       const i32x4 a = *reinterpret_cast<const i32x4*>(b + rl * ROWB + swz(rl, 2 * u + slot) * 16);
@@ -311,8 +315,11 @@ void proj_kernel(ProjArgs p) {
     for (int jj = 0; jj < 8; ++jj) {
       const int i0 = 2 * jj, i1 = 2 * jj + 1;
       const int ra = acc_row(i0, slot), rb = acc_row(i1, slot);
-      const float v0 = ((mword >> ra) & 1u) ? 0.f : acc[i0] + bias;
-      const float v1 = ((mword >> rb) & 1u) ? 0.f : acc[i1] + bias;
+      float v0 = acc[i0], v1 = acc[i1];
+      if (mword != 0u) {  // wave-uniform: blocks without padded rows skip the selects
+        v0 = ((mword >> ra) & 1u) ? 0.f : v0;
+        v1 = ((mword >> rb) & 1u) ? 0.f : v1;
+      }
       // even lane keeps row ra and takes the partner's (row ra, c+1);
       // odd lane keeps row rb and takes the partner's (row rb, c-1).
       const float x = swap_pair_lane(odd ? v0 : v1);
