@@ -49,6 +49,8 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
   constexpr int kVec = C::kVec;
   constexpr int kWords = C::kWords;
   constexpr bool kStatic = G > 0;
+  // NoAcc: grad_loc / grad_attn only (grad_value comes from the owner kernel).
+  constexpr bool kScatter = A::kBytes > 0;
   // Accumulator byte offset = value byte offset * kAccScale.
   constexpr uint32_t kAccScale = A::kBytes / T::kBytes;
 
@@ -88,7 +90,7 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
   C::load(rg, (uint32_t)pair * (uint32_t)(p.D * T::kBytes) + chb, gv);
   using Sc = Scatter<T, A, CB>;
   float sg[Sc::kSlots];
-  Sc::load_g(p, pair, ch, live, sg);
+  if constexpr (kScatter) Sc::load_g(p, pair, ch, live, sg);
   float delta = 0.f;  // fused: <grad_out, out> of this lane's pair
   if constexpr (FUSED) {
     float ov[kVec];
@@ -173,11 +175,13 @@ __global__ __launch_bounds__(kBlock) void bwd_kernel(Params p) {
           }
           // Atomics interleaved with the next samples' gathers measured
           // faster than issuing them all after the gathers (decoder preset).
-          if (live) {
-            Sc::add(ra, o[u].x * kAccScale, ch, p.g_real, a * w00, sg, det_s);
-            Sc::add(ra, o[u].y * kAccScale, ch, p.g_real, a * w01, sg, det_s);
-            Sc::add(ra, o[u].z * kAccScale, ch, p.g_real, a * w10, sg, det_s);
-            Sc::add(ra, o[u].w * kAccScale, ch, p.g_real, a * w11, sg, det_s);
+          if constexpr (kScatter) {
+            if (live) {
+              Sc::add(ra, o[u].x * kAccScale, ch, p.g_real, a * w00, sg, det_s);
+              Sc::add(ra, o[u].y * kAccScale, ch, p.g_real, a * w01, sg, det_s);
+              Sc::add(ra, o[u].z * kAccScale, ch, p.g_real, a * w10, sg, det_s);
+              Sc::add(ra, o[u].w * kAccScale, ch, p.g_real, a * w11, sg, det_s);
+            }
           }
         }
       }
@@ -216,6 +220,7 @@ hipError_t dispatch(const Shape& s, const Params& p, hipStream_t st) {
     case 81601: return launch_one<T, A, 8, 16, 1, FUSED>(p, st);
     case 161601: return launch_one<T, A, 16, 16, 1, FUSED>(p, st);
     case 160404: return launch_one<T, A, 16, 4, 4, FUSED>(p, st);
+    case 160804: return launch_one<T, A, 16, 8, 4, FUSED>(p, st);
     default: break;
   }
   if (s.cb == 16) return launch_one<T, A, 16, 0, 0, FUSED>(p, st);
@@ -230,6 +235,14 @@ hipError_t dispatch(const Shape& s, const Params& p, hipStream_t st) {
 template <bool FUSED>
 hipError_t dispatch_dtype(int dtype, AccMode acc, const Shape& s, const Params& p,
                           hipStream_t st) {
+  if (acc == kAccNone) {
+    switch (dtype) {
+      case kF32: return dispatch<F32, NoAcc, FUSED>(s, p, st);
+      case kF16: return dispatch<F16, NoAcc, FUSED>(s, p, st);
+      case kBF16: return dispatch<BF16, NoAcc, FUSED>(s, p, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (dtype) {
     case kF32:
       return acc == kAccI64 ? dispatch<F32, I64, FUSED>(s, p, st)

@@ -1,0 +1,533 @@
+// Owner-computes grad_value for gfx950: every element of grad_value is
+// written exactly once, with plain stores -- no atomics, no zero-fill.
+//
+// The reference scatters grad_value[corner] += A * w_c * grad_out[pair] with
+// atomics (src/msda_triton/kernels.py:278-291) into a zeroed buffer
+// (src/msda_triton/ops.py:76-77).  Measured on MI355X, those buffer atomics
+// are forwarded past L2 and complete at a fixed chip-wide rate of requests,
+// and the zero-fill alone writes the whole tensor once; at decoder sizes the
+// two make up ~85% of the backward.  When a (b, m, level) holds few samples
+// (Q * K <= kOwnCap: decoder cross-attention, Q ~ 300-900), the same sums
+// can be formed by the rows' owners instead:
+//
+//   one workgroup owns (batch b, head m, band [lo, hi) of the pixel axis);
+//   it evaluates the bilinear geometry of every sample of (b, m) on each
+//   level that meets the band (Q * K samples, <= 8 per lane, kept in
+//   registers), counts the in-map corners that land in the band per row
+//   (integer LDS atomics), turns the counts into CSR offsets (block scan),
+//   fills the CSR with (A * w_c, query) entries, and then gives each row to
+//   a team of G lanes that sums its entries' grad_out chunks (staged once in
+//   LDS) in fp32 registers and stores the row -- zeros for rows no sample
+//   touches.
+//
+// The sums are the reference's, accumulated in fp32 and rounded once, in
+// every mode (the fp32_grad_accum choice is moot here).  Their order within a
+// row follows the CSR fill, so grad_value is not bitwise reproducible across
+// runs (like the reference's atomics); grad_loc / grad_attn come from the
+// direct backward kernel launched without its scatter.
+//
+// Bands: for a standard level table (start_0 = 0, start_{l+1} = start_l +
+// H_l W_l, levels covering [0, S): what level_start_index = None gives) each
+// level l is split into n_l = min(H_l W_l, max(ceil(H_l W_l / own_rows),
+// own_split)) bands, so coarse levels -- few pixels, as many corner entries
+// as the fine ones -- are shared by several workgroups.  Any other table
+// gets uniform bands of own_rows pixels; a band then may meet several levels
+// (handled one level per round: the first round stores every row, later
+// rounds add into the rows they touch -- the workgroup is their only
+// writer) or none (rows stored as zeros).
+#include "msda_launch.h"
+
+namespace msda {
+
+namespace {
+
+constexpr int kOwnRows = 4 * kBlock;       // pixels per band, at most (4 per lane in the scan)
+constexpr int kOwnCap = 2048;              // CSR entries per sub-band; path needs Q * K <= it
+constexpr int kOwnEntryTarget = 1024;      // corner entries per band the level split aims at
+constexpr int kOwnGBytes = 5 * 16 * kBlock;  // staged grad_out rows (Q * D * elem), at most
+
+// Band [lo, hi) of group gi of a (b, m); false for groups past the last band.
+__device__ bool own_band(const Params& p, const LevelTable& lt, int gi, int& lo, int& hi) {
+  bool standard = true;
+  int64_t acc = 0;
+  for (int l = 0; l < p.L; ++l) {
+    if (lt.h[l] < 0 || lt.w[l] < 0 || (int64_t)lt.start[l] != acc) standard = false;
+    acc += (int64_t)lt.h[l] * lt.w[l];
+  }
+  if (acc != (int64_t)p.S) standard = false;
+  if (standard) {
+    for (int l = 0; l < p.L; ++l) {
+      const int hw = lt.h[l] * lt.w[l];
+      if (hw == 0) continue;
+      int n = (hw + p.own_rows - 1) / p.own_rows;
+      if (n < p.own_split) n = p.own_split;
+      if (n > hw) n = hw;
+      if (gi < n) {
+        const int size = (hw + n - 1) / n;
+        lo = lt.start[l] + gi * size;
+        hi = min(lo + size, lt.start[l] + hw);
+        return lo < hi;
+      }
+      gi -= n;
+    }
+    return false;
+  }
+  lo = gi * p.own_rows;
+  hi = min(lo + p.own_rows, p.S);
+  return lo < hi;
+}
+
+// Exclusive prefix sum over the workgroup; `tot` receives the total.
+__device__ __forceinline__ int own_scan(int v, int* wsum, int* tot) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  if (lane == kWave - 1) wsum[wave] = x;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wsum[w];
+  *tot = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  return base + x - v;
+}
+
+// Image coordinates (x = loc_x * W - 0.5; fused: ref_x * W + offset_x - 0.5)
+// and weight A (fused: exp(logit - lse)) of one sample, rounded exactly as
+// make_sample_at rounds them.  Loads go through buffer descriptors: an
+// out-of-range offset (a lane past the last sample) reads zeros, no branch.
+struct OwnRsrc {
+  __amdgpu_buffer_rsrc_t loc, attn, ref, lse;
+};
+
+template <class T, bool FUSED>
+__device__ __forceinline__ void own_sample(const Params& p, const OwnRsrc& rs, uint32_t pair,
+                                           uint32_t s, uint32_t bq, uint32_t l, bool valid,
+                                           float fw, float fh, float& x, float& y, float& a) {
+  const uint32_t pi = pair * (uint32_t)p.LK + s;
+  const uint32_t dead = valid ? 0u : 0x80000000u;
+  float u, v, w;
+  if constexpr (T::kBytes == 4) {
+    const i32x2 xy = __builtin_amdgcn_raw_buffer_load_b64(rs.loc, (pi * 8u) | dead, 0, 0);
+    u = __int_as_float(xy[0]);
+    v = __int_as_float(xy[1]);
+    w = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs.attn, (pi * 4u) | dead, 0, 0));
+  } else {
+    unpack2<T>((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs.loc, (pi * 4u) | dead, 0, 0), u, v);
+    w = unpack1<T>((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs.attn, (pi * 2u) | dead, 0, 0));
+  }
+  if constexpr (FUSED) {
+    const uint32_t ri = p.ref_levels ? bq * (uint32_t)p.L + l : bq;
+    float rx, ry;
+    if constexpr (T::kBytes == 4) {
+      const i32x2 r2 = __builtin_amdgcn_raw_buffer_load_b64(rs.ref, (ri * 8u) | dead, 0, 0);
+      rx = __int_as_float(r2[0]);
+      ry = __int_as_float(r2[1]);
+    } else {
+      unpack2<T>((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs.ref, (ri * 4u) | dead, 0, 0), rx,
+                 ry);
+    }
+    const float lse =
+        __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs.lse, (pair * 4u) | dead, 0, 0));
+    x = __fsub_rn(__fmaf_rn(rx, fw, u), 0.5f);
+    y = __fsub_rn(__fmaf_rn(ry, fh, v), 0.5f);
+    a = expf(w - lse);
+  } else {
+    x = __fsub_rn(__fmul_rn(u, fw), 0.5f);
+    y = __fsub_rn(__fmul_rn(v, fh), 0.5f);
+    a = w;
+  }
+  if (!valid) x = y = -4.f;  // a cell outside every map
+}
+
+// Corner cell of (x, y): pixel index of corner 00, fractions, and the bits
+// of the corners that lie in the map and in [lo, hi) (bit c: corner c =
+// 00, 01, 10, 11 at pixel pix + (c & 1) + (c >> 1) * W).  Same floors and
+// validity as make_sample_at.
+__device__ __forceinline__ uint32_t own_cell(float x, float y, int W, int H, int st, int lo, int hi,
+                                             int& pix, float& lx, float& ly) {
+  float x0f = floorf(x), y0f = floorf(y);
+  lx = x - x0f;
+  ly = y - y0f;
+  x0f = fminf(fmaxf(x0f, -2.f), (float)W + 1.f);
+  y0f = fminf(fmaxf(y0f, -2.f), (float)H + 1.f);
+  const int x0 = (int)x0f, y0 = (int)y0f;
+  const bool vx0 = (x0 >= 0) & (x0 < W), vx1 = (x0 >= -1) & (x0 < W - 1);
+  const bool vy0 = (y0 >= 0) & (y0 < H), vy1 = (y0 >= -1) & (y0 < H - 1);
+  pix = st + y0 * W + x0;
+  const bool c0 = vy0 & vx0 & (pix >= lo) & (pix < hi);
+  const bool c1 = vy0 & vx1 & (pix + 1 >= lo) & (pix + 1 < hi);
+  const bool c2 = vy1 & vx0 & (pix + W >= lo) & (pix + W < hi);
+  const bool c3 = vy1 & vx1 & (pix + W + 1 >= lo) & (pix + W + 1 < hi);
+  return (uint32_t)c0 | (uint32_t)c1 << 1 | (uint32_t)c2 << 2 | (uint32_t)c3 << 3;
+}
+
+constexpr int kOwnQBits = 11;  // query index in a CSR entry (Q <= Q * K <= kOwnCap)
+static_assert(kOwnCap <= (1 << kOwnQBits), "query index field");
+
+// T: storage dtype; NS: samples per lane and level (NS * kBlock >= Q * K).
+// p.g_rt lanes (a power of two, g_real of them live) cover a value row in
+// 16-byte chunks.  ~39 KB of LDS and <= 128 VGPRs: four workgroups per CU.
+template <class T, int NS, bool FUSED>
+__global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
+  using C = Chunk<T, 16>;
+  constexpr int kVec = C::kVec;
+  constexpr int kGIt = kOwnGBytes / 16 / kBlock;  // staged 16-byte chunks per lane
+  static_assert(kOwnRows == 4 * kBlock, "four rows per lane in the scan");
+  static_assert(kOwnGBytes % (16 * kBlock) == 0, "whole staging rounds");
+  static_assert(4 * NS * kBlock < 65536, "16-bit CSR offsets");
+
+  __shared__ LevelTable lt;
+  __shared__ uint16_t s_off[kOwnRows + 1];  // CSR offsets (exclusive prefix sum of the counts)
+  // Entries per row (count pass); then the CSR entries (A * w_c, query |
+  // local row << kOwnQBits), rows contiguous; then, after the entries are
+  // read, each team's piece of the row it continues from the slice before.
+  __shared__ union {
+    int cnt[kOwnRows];
+    float2 csr[kOwnCap];
+    float piece[kBlock * kVec];
+  } u;
+  __shared__ int s_wsum[kBlock / kWave];
+  __shared__ __align__(16) uint8_t s_g[kOwnGBytes];  // grad_out rows of (b, m): Q x D * elem
+
+  const int tid = threadIdx.x;
+  // Grid: bid = 8 k + x runs on XCD x (round-robin dispatch).  Band group
+  // bg = (k / M) * 8 + x and head m = k % M: the heads of a band share an
+  // XCD (whole 128-byte lines of grad_value meet in its L2), XCDs get
+  // interleaved band groups, and bands past the last level (idle groups)
+  // come last in dispatch order.
+  const int x8 = blockIdx.x & 7, k8 = blockIdx.x >> 3;
+  const int m = k8 % p.M;
+  const int bg = (k8 / p.M) * 8 + x8;
+  const int nb = p.npairs / (p.Q * p.M);
+  const int b = bg % nb;
+  const int gi = bg / nb;
+  if (gi >= p.own_groups) return;  // grid padding
+
+  const int rowb = p.D * T::kBytes;  // g_real * 16 (path condition)
+  const int nsmp = p.Q * p.K;
+  // Stage grad_out[b, :, m, :]: loads issued before the level table's round
+  // trip, written to LDS after it (chunk k of the stage is its byte k * 16).
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.grad_out, p.gout_bytes);
+  const uint32_t gq0 = ((uint32_t)b * (uint32_t)p.Q * (uint32_t)p.M + (uint32_t)m) * (uint32_t)rowb;
+  const uint32_t gqs = (uint32_t)p.M * (uint32_t)rowb;  // grad_out stride between queries
+  const int nchunk = p.Q * p.g_real;
+  i32x4 graw[kGIt];
+#pragma unroll
+  for (int k = 0; k < kGIt; ++k) {
+    const int kk = tid + k * kBlock;
+    const int q = kk / p.g_real;
+    const uint32_t off = kk < nchunk ? gq0 + (uint32_t)q * gqs + (uint32_t)(kk - q * p.g_real) * 16u
+                                     : 0x80000000u;
+    graw[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0);
+  }
+  load_levels(p, lt);
+#pragma unroll
+  for (int k = 0; k < kGIt; ++k) {
+    const int kk = tid + k * kBlock;
+    if (kk < nchunk) *reinterpret_cast<i32x4*>(s_g + kk * 16) = graw[k];
+  }
+  __syncthreads();
+  int lo, hi;
+  if (!own_band(p, lt, gi, lo, hi)) return;  // same answer in every lane
+
+  const int G = p.g_rt, lg = p.own_lg;  // lanes per row and its log2
+  const int kTeams = kBlock >> lg;
+  const int team = tid >> lg, ch = tid & (G - 1);
+  const bool live = ch < p.g_real;
+  const int chg = live ? ch * 16 : 0;  // padding lanes read a live chunk, store nothing
+  const int nrows = hi - lo;
+  const int e = T::kBytes;
+  const uint32_t nsp = (uint32_t)p.npairs * (uint32_t)p.LK;  // samples in the slice
+  const OwnRsrc rs = {make_rsrc(p.loc, nsp * 2u * e), make_rsrc(p.attn, nsp * e),
+                      make_rsrc(p.ref, FUSED ? p.ref_bytes : 0u),
+                      make_rsrc(p.lse, FUSED ? (uint32_t)p.npairs * 4u : 0u)};
+  char* const gval = static_cast<char*>(p.grad_acc);
+  const uint64_t row0 = (uint64_t)b * (uint32_t)p.S;  // pixel rows of batch b
+  auto row_ptr = [&](int r) {
+    return gval + ((row0 + (uint32_t)(lo + r)) * (uint32_t)p.M + m) * (uint32_t)rowb + ch * 16;
+  };
+  // Store a finished row sum: plain in the first round, added to the row's
+  // earlier value in later rounds (this workgroup is the row's only writer).
+  auto put = [&](int r, const float (&acc)[kVec], bool written) {
+    if (!live) return;
+    char* dst = row_ptr(r);
+    float v[kVec];
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) v[k] = acc[k];
+    if (written) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(dst);
+      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+      float old[kVec];
+      C::unpack(w4, old);
+#pragma unroll
+      for (int k = 0; k < kVec; ++k) v[k] += old[k];
+    }
+    C::store(dst, v);
+  };
+
+  bool written = false;
+  for (int l = 0; l < p.L; ++l) {
+    const int H = lt.h[l], W = lt.w[l], st = lt.start[l];
+    if (H <= 0 || W <= 0) continue;
+    if ((int64_t)st >= hi || (int64_t)st + (int64_t)H * W <= lo) continue;
+    const float fw = (float)W, fh = (float)H;
+
+    // Coordinates and weights of this lane's samples j = tid + i * kBlock of
+    // (b, m, l), all parameter loads in flight together.
+    float sx[NS], sy[NS], sa[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const int j = tid + i * kBlock;
+      const bool valid = j < nsmp;
+      const uint32_t q = fdiv((uint32_t)(valid ? j : 0), p.div_k);
+      const uint32_t bq = (uint32_t)b * (uint32_t)p.Q + q;
+      own_sample<T, FUSED>(p, rs, bq * (uint32_t)p.M + m, (uint32_t)(l * p.K + j) - q * p.K, bq,
+                           (uint32_t)l, valid, fw, fh, sx[i], sy[i], sa[i]);
+    }
+    for (int r = tid; r < nrows; r += kBlock) u.cnt[r] = 0;
+    __syncthreads();  // counts zeroed (and, in later rounds, the last pieces read)
+
+    // 1. Entries per row; the count an entry finds is its rank in the row.
+    uint32_t rank[NS * 2];  // 16-bit ranks, corners 2h and 2h + 1 of a sample in word h
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      int pix;
+      float lx, ly;
+      const uint32_t bits = own_cell(sx[i], sy[i], W, H, st, lo, hi, pix, lx, ly);
+      uint32_t rk[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        rk[c] = 0;
+        if (bits & (1u << c)) rk[c] = atomicAdd(&u.cnt[pix + (c & 1) + (c >> 1) * W - lo], 1);
+      }
+      rank[2 * i] = rk[0] | rk[1] << 16;
+      rank[2 * i + 1] = rk[2] | rk[3] << 16;
+    }
+    __syncthreads();
+
+    // 2. CSR offsets.
+    {
+      int c4[4], sum = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = tid * 4 + k;
+        c4[k] = r < nrows ? u.cnt[r] : 0;
+        sum += c4[k];
+      }
+      int tot;
+      int ex = own_scan(sum, s_wsum, &tot);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = tid * 4 + k;
+        if (r < nrows) s_off[r] = (uint16_t)ex;
+        ex += c4[k];
+      }
+      if (tid == 0) s_off[nrows] = (uint16_t)tot;
+    }
+    __syncthreads();  // offsets written, counts dead (the CSR reuses them)
+
+    // 3. Sub-bands of at most kOwnCap entries: one unless many samples pile
+    // onto the band.  A row alone never exceeds it: a sample puts at most one
+    // corner on a row, and Q * K <= kOwnCap.
+    for (int r0 = 0; r0 < nrows;) {
+      const int base = s_off[r0];
+      int a = nrows, z = nrows;
+      if (s_off[nrows] - base > kOwnCap) {  // binary search for the sub-band's end
+        a = r0 + 1;
+        while (a < z) {
+          const int mid = (a + z + 1) >> 1;
+          if (s_off[mid] - base <= kOwnCap) {
+            a = mid;
+          } else {
+            z = mid - 1;
+          }
+        }
+      }
+      const int r1 = a;
+      const int ne = s_off[r1] - base;
+
+      // Fill: entry slot = row offset + rank.  The geometry is recomputed
+      // from (x, y, A) rather than hoisted out of the sub-band loop by the
+      // compiler: the cells and coefficients of all NS samples would
+      // otherwise stay live (~100 registers).
+#pragma unroll
+      for (int i = 0; i < NS; ++i) asm volatile("" : "+v"(sx[i]), "+v"(sy[i]), "+v"(sa[i]));
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        int pix;
+        float lx, ly;
+        const uint32_t bits = own_cell(sx[i], sy[i], W, H, st, lo, hi, pix, lx, ly);
+        const uint32_t q = fdiv((uint32_t)min(tid + i * kBlock, nsmp - 1), p.div_k);
+        const float mx = 1.f - lx, my = 1.f - ly;
+        // The four row offsets are read unconditionally (row 0 stands in
+        // for corners that add nothing) so that they share one LDS wait.
+        int r[4], o[4];
+        bool in[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          r[c] = pix + (c & 1) + (c >> 1) * W - lo;
+          in[c] = (bits & (1u << c)) && r[c] >= r0 && r[c] < r1;
+          o[c] = s_off[in[c] ? r[c] : 0];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (in[c]) {
+            const float w = (c & 1 ? lx : mx) * (c >> 1 ? ly : my);
+            const int slot = o[c] - base + (int)((rank[2 * i + (c >> 1)] >> (16 * (c & 1))) & 0xffffu);
+            u.csr[slot] = make_float2(sa[i] * w, __int_as_float((int)q | r[c] << kOwnQBits));
+          }
+        }
+      }
+      __syncthreads();
+
+      // Rows without entries: zeros in the first round, untouched later.
+      if (!written) {
+        const float zero[kVec] = {};
+        for (int r = r0 + team; r < r1; r += kTeams)
+          if (s_off[r + 1] == s_off[r]) put(r, zero, false);
+      }
+
+      // Entries: team t sums slice [t * cs, (t + 1) * cs) of the CSR.  A row
+      // whose entries all lie in the slice is stored by the team; the piece
+      // of a row that started in an earlier slice waits in `first`, the
+      // piece of a row that runs on into later slices in `tail`.
+      const int cs = (ne + kTeams - 1) / kTeams;
+      const int e_lo = min(team * cs, ne), e_hi = min(e_lo + cs, ne);
+      float first[kVec], acc[kVec];
+      bool has_first = false;
+      int tail_row = -1;
+#pragma unroll
+      for (int k = 0; k < kVec; ++k) first[k] = acc[k] = 0.f;
+      if (e_lo < e_hi) {
+        int cur = __float_as_int(u.csr[e_lo].y) >> kOwnQBits;
+        auto flush = [&]() {
+          const int rs0 = s_off[cur] - base, re0 = s_off[cur + 1] - base;
+          if (rs0 < e_lo) {
+#pragma unroll
+            for (int k = 0; k < kVec; ++k) first[k] = acc[k];
+            has_first = true;
+          } else if (re0 > e_hi) {
+            tail_row = cur;  // acc stays the tail
+          } else {
+            put(cur, acc, written);
+          }
+        };
+        for (int e0 = e_lo; e0 < e_hi; e0 += 4) {
+          float2 en[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) en[k] = u.csr[min(e0 + k, e_hi - 1)];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            if (e0 + k < e_hi) {
+              const int bits = __float_as_int(en[k].y);
+              const int r = bits >> kOwnQBits;
+              if (r != cur) {
+                flush();
+#pragma unroll
+                for (int v = 0; v < kVec; ++v) acc[v] = 0.f;
+                cur = r;
+              }
+              const uint4 raw = *reinterpret_cast<const uint4*>(
+                  s_g + (bits & ((1 << kOwnQBits) - 1)) * rowb + chg);
+              const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+              float gv[kVec];
+              C::unpack(w4, gv);
+#pragma unroll
+              for (int v = 0; v < kVec; ++v) acc[v] += en[k].x * gv[v];
+            }
+          }
+        }
+        flush();
+      }
+      __syncthreads();  // every entry read: the pieces may overwrite the CSR
+      if (has_first) {
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) u.piece[(team * G + ch) * kVec + k] = first[k];
+      }
+      __syncthreads();
+      if (tail_row >= 0) {  // add the pieces of the later slices, in order
+        const int t2 = (s_off[tail_row + 1] - base - 1) / cs;
+        for (int t = team + 1; t <= t2; ++t) {
+#pragma unroll
+          for (int k = 0; k < kVec; ++k) acc[k] += u.piece[(t * G + ch) * kVec + k];
+        }
+        put(tail_row, acc, written);
+      }
+      __syncthreads();  // pieces read before the next sub-band's fill
+      r0 = r1;
+    }
+    // Later rounds read back rows this workgroup stored: let the stores land.
+    __builtin_amdgcn_s_waitcnt(0);
+    written = true;
+  }
+
+  if (!written) {  // no level meets the band: its rows are zero
+    const float zero[kVec] = {};
+    for (int r = team; r < nrows; r += kTeams) put(r, zero, false);
+  }
+}
+
+template <class T, int NS, bool FUSED>
+hipError_t launch_ns(const Params& p, hipStream_t st) {
+  hipLaunchKernelGGL((owner_kernel<T, NS, FUSED>), dim3(p.nblocks), dim3(kBlock), 0, st, p);
+  return hipGetLastError();
+}
+
+template <class T, bool FUSED>
+hipError_t launch_t(const Params& p, hipStream_t st) {
+  switch ((p.Q * p.K + kBlock - 1) / kBlock) {
+    case 1: return launch_ns<T, 1, FUSED>(p, st);
+    case 2: return launch_ns<T, 2, FUSED>(p, st);
+    case 3: return launch_ns<T, 3, FUSED>(p, st);
+    case 4: return launch_ns<T, 4, FUSED>(p, st);
+    case 5: return launch_ns<T, 5, FUSED>(p, st);
+    case 6: return launch_ns<T, 6, FUSED>(p, st);
+    case 7: return launch_ns<T, 7, FUSED>(p, st);
+    case 8: return launch_ns<T, 8, FUSED>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool owner_plan(int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L, int elem_bytes,
+                Params* p) {
+  const int64_t rowb = D * elem_bytes;
+  if (rowb <= 0 || rowb % 16 != 0 || rowb / 16 > 16) return false;
+  if (Q * K <= 0 || Q * K > kOwnCap || Q * rowb > kOwnGBytes) return false;
+  if (S <= 0 || L <= 0) return false;
+  const int64_t split = (4 * Q * K + kOwnEntryTarget - 1) / kOwnEntryTarget;
+  const int64_t groups = (S + kOwnRows - 1) / kOwnRows + L * (1 + split);
+  if (groups * (int64_t)p->M * 64 >= (1ll << 31)) return false;
+  p->own_rows = kOwnRows;
+  p->own_split = (int32_t)split;
+  p->own_groups = (int32_t)groups;
+  p->g_real = (int32_t)(rowb / 16);
+  int g = 1, lg = 0;
+  while (g < p->g_real) {
+    g <<= 1;
+    ++lg;
+  }
+  p->g_rt = g;
+  p->own_lg = lg;
+  return true;
+}
+
+hipError_t launch_owner(int dtype, bool fused, const Params& p0, hipStream_t st) {
+  Params p = p0;
+  const int64_t nb = p.npairs / ((int64_t)p.Q * p.M);  // batch elements in the slice
+  const int64_t groups = (nb * p.own_groups + 7) / 8 * 8;  // band groups, padded to the XCDs
+  p.nblocks = (int32_t)(groups * p.M);
+  if (p.nblocks == 0) return hipSuccess;
+  switch (dtype) {
+    case kF32: return fused ? launch_t<F32, true>(p, st) : launch_t<F32, false>(p, st);
+    case kF16: return fused ? launch_t<F16, true>(p, st) : launch_t<F16, false>(p, st);
+    case kBF16: return fused ? launch_t<BF16, true>(p, st) : launch_t<BF16, false>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace msda

@@ -94,6 +94,11 @@ static int bwd_cb_pref() { return env_int("MSDA_BWD_CB"); }
 static bool bwd_priv_enabled() {
   return getenv("MSDA_BWD_PRIV") == nullptr || env_int("MSDA_BWD_PRIV") != 0;
 }
+// MSDA_BWD_OWNER=0: atomic backward even where the owner-computes one applies.
+static bool bwd_owner_enabled() {
+  return getenv("MSDA_BWD_OWNER") == nullptr || env_int("MSDA_BWD_OWNER") != 0;
+}
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 static int elem_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
 
@@ -227,17 +232,27 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
     return MSDA_ERR_INVALID_ARGUMENT;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool det = det_workspace != nullptr && n_val > 0;
+  const bool compute = n_smp > 0 && n_out > 0 && d.S > 0;
+  // Owner-computes grad_value (few samples per (b, m, level)): every element
+  // stored once in fp32-accumulated form, so neither the zero-fill nor the
+  // fp32 scratch is used.
+  Params own = {};
+  base_params(d, 0, d.B, dtype, &own);
+  const bool owner = compute && !det && bwd_owner_enabled() && aligned16(grad_output) &&
+                     aligned16(grad_value) && owner_plan(d.Q, d.K, d.D, d.S, d.L, e, &own);
   // fp32 accumulation is only a separate path for half storage.
-  const bool fp32_acc = !det && grad_value_accum != nullptr && dtype != kF32 && n_val > 0;
+  const bool fp32_acc =
+      !owner && !det && grad_value_accum != nullptr && dtype != kF32 && n_val > 0;
   const AccMode mode = det ? kAccI64 : fp32_acc ? kAccF32 : kAccNative;
   void* acc = det ? det_workspace : fp32_acc ? static_cast<void*>(grad_value_accum) : grad_value;
   const int acc_e = det ? 8 : fp32_acc ? 4 : e;
   uint32_t* det_max =
       det ? reinterpret_cast<uint32_t*>(static_cast<char*>(det_workspace) + n_val * 8) : nullptr;
 
-  rc = status(launch_zero(acc, (uint64_t)(n_val * acc_e) + (det ? 8u : 0u), st));
-  if (rc != MSDA_OK) return rc;
-  const bool compute = n_smp > 0 && n_out > 0 && d.S > 0;
+  if (!owner) {
+    rc = status(launch_zero(acc, (uint64_t)(n_val * acc_e) + (det ? 8u : 0u), st));
+    if (rc != MSDA_OK) return rc;
+  }
   if (det && compute) {
     rc = status(launch_det_max(dtype, f ? nullptr : attn, f ? 0 : (uint64_t)n_smp, grad_output,
                                (uint64_t)n_out, det_max, st));
@@ -252,9 +267,12 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
     if (rc == MSDA_OK) rc = status(launch_zero(grad_attn, (uint64_t)(n_smp * e), st));
     if (rc != MSDA_OK) return rc;
   } else if (compute) {
+    // The owner path runs the direct kernel without its scatter: no atomics
+    // to spread over pairs, so it takes the forward's launch shape.
     Shape sh;
-    if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, true, bwd_ts_pref(),
-                      bwd_cb_pref(), &sh))
+    if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, !owner,
+                      owner ? fwd_ts_pref() : bwd_ts_pref(),
+                      owner ? fwd_cb_pref() : bwd_cb_pref(), &sh))
       return MSDA_ERR_UNSUPPORTED_SHAPE;
     const int64_t bs = slice_batch(d);
     if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
@@ -282,6 +300,23 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
         p.lse = f->lse + b0 * d.Q * d.M;
         p.out_fwd = at(f->output, oo, e);
         p.ref_levels = f->ref_levels;
+      }
+      if (owner) {
+        Params po = p;
+        po.grad_acc = at(grad_value, vo, e);
+        po.own_rows = own.own_rows;
+        po.own_split = own.own_split;
+        po.own_groups = own.own_groups;
+        po.g_real = own.g_real;
+        po.g_rt = own.g_rt;
+        po.own_lg = own.own_lg;
+        if (f) po.ref_bytes = (uint32_t)(nb * ref_per_b * e);
+        rc = status(launch_owner(dtype, f != nullptr, po, st));
+        if (rc != MSDA_OK) return rc;
+        finish_params(sh, kBwdRecords, &p);
+        rc = status(launch_backward(dtype, kAccNone, f != nullptr, sh, p, st));
+        if (rc != MSDA_OK) return rc;
+        continue;
       }
       finish_params(sh, kBwdRecords, &p);
       if (bwd_priv_enabled() && priv_supported(sh, (int)d.D, (int)d.K, e)) {
@@ -434,7 +469,6 @@ extern "C" int msda_fused_backward_deterministic(
 // ---------------------------------------------------------------------------
 // Projections either side of the operator.
 // ---------------------------------------------------------------------------
-static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 struct ProjDims {
   int64_t rows, in, out, split;

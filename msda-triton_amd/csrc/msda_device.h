@@ -82,6 +82,12 @@ struct I64 {
   static constexpr int kBytes = 8;
   static constexpr int kCode = -1;
 };
+// "Accumulator" of a backward launch that scatters nothing (grad_loc and
+// grad_attn only; grad_value is written by the owner kernel).
+struct NoAcc {
+  static constexpr int kBytes = 0;
+  static constexpr int kCode = -2;
+};
 
 // Two storage elements packed in one 32-bit word -> two floats.
 template <class T>
@@ -344,6 +350,11 @@ struct Params {
   int32_t ts_rt;    // runtime TS (generic kernels)
   int32_t nq;       // deduplicating backward: queries per workgroup
   int32_t nqblk;    //   query blocks per (b, m, l)
+  int32_t own_rows;    // owner backward: most rows per band (<= kOwnRows)
+  int32_t own_split;   //   least bands per level (entry balance)
+  int32_t own_groups;  //   bands (workgroups) per (b, m) in the grid
+  int32_t own_lg;      //   log2 of the lanes per row (g_rt)
+  uint32_t ref_bytes;  //   fused: num_records of the reference points
   FastDiv div_qm, div_m, div_k, div_d;
 };
 
@@ -445,6 +456,8 @@ __device__ __forceinline__ void pair_lse(const Params& p, int pair0, int ppb, in
 struct Sample {
   uint32_t off[4];  // element offsets of corners 00, 01, 10, 11 (kOobElem if outside)
   float lx, ly, a, fw, fh;
+  int32_t pix;      // pixel index (start + y0 * W + x0) of corner 00; meaningful for in-map corners
+  uint32_t vmask;   // bit c set when corner c lies in the map
 };
 
 //
@@ -466,6 +479,8 @@ __device__ __forceinline__ Sample make_sample_at(const Params& p, uint32_t pair,
   if (!valid) {
     r.off[0] = r.off[1] = r.off[2] = r.off[3] = kOobElem;
     r.lx = r.ly = r.a = r.fw = r.fh = 0.f;
+    r.pix = 0;
+    r.vmask = 0;
     return r;
   }
   const uint32_t bq = fdiv(pair, p.div_m);
@@ -507,6 +522,9 @@ __device__ __forceinline__ Sample make_sample_at(const Params& p, uint32_t pair,
   r.a = a;
   r.fw = fw;
   r.fh = fh;
+  r.pix = st + y0 * W + x0;
+  r.vmask = (uint32_t)(vy0 & vx0) | (uint32_t)(vy0 & vx1) << 1 | (uint32_t)(vy1 & vx0) << 2 |
+            (uint32_t)(vy1 & vx1) << 3;
   return r;
 }
 

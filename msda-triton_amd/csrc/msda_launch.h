@@ -31,8 +31,9 @@ bool choose_shape(int row_bytes, int lk, int64_t npairs, bool backward, int ts_p
 void finish_params(const Shape& s, int max_records, Params* p);
 
 // grad_value accumulator of the backward: the storage dtype's own atomics,
-// an fp32 scratch, or int64 fixed point (deterministic; see det_scale).
-enum AccMode : int { kAccNative = 0, kAccF32 = 1, kAccI64 = 2 };
+// an fp32 scratch, int64 fixed point (deterministic; see det_scale), or none
+// (grad_loc / grad_attn only, grad_value written by the owner kernel).
+enum AccMode : int { kAccNative = 0, kAccF32 = 1, kAccI64 = 2, kAccNone = 3 };
 
 // `fused`: the fused front-end variants (offsets + logits instead of
 // locations + weights; see Params).
@@ -45,6 +46,13 @@ bool priv_supported(const Shape& s, int D, int K, int elem_bytes);
 void priv_params(const Shape& s, int elem_bytes, Params* p);
 hipError_t launch_backward_priv(int dtype, AccMode acc, bool fused, const Shape& s,
                                 const Params& p, hipStream_t st);
+// Owner-computes grad_value (msda_backward_owner.hip): every element written
+// once with plain stores, no atomics and no zero-fill; for calls with few
+// samples per (b, m, level).  owner_plan fills the owner fields of `p` and
+// returns false when the call does not qualify.
+bool owner_plan(int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L, int elem_bytes,
+                Params* p);
+hipError_t launch_owner(int dtype, bool fused, const Params& p, hipStream_t st);
 // Fused front-end: reference-point gradient from the offset gradients, one
 // wave per (b, q) of the nbq in the call.
 hipError_t launch_ref_grad(int dtype, const Params& p, uint64_t nbq, hipStream_t st);

@@ -42,7 +42,7 @@ struct Scatter {
   static constexpr int kVec = CB / T::kBytes;
   static constexpr int kWordBytes = A::kBytes == 8 ? 8 : 4;
   static constexpr int kWordsPerLane = kVec * A::kBytes / kWordBytes;  // 0: odd-D half rows
-  static constexpr int kElemsPerWord = kWordBytes / A::kBytes;
+  static constexpr int kElemsPerWord = A::kBytes > 0 ? kWordBytes / A::kBytes : 1;
   static constexpr int kSlots = kWordsPerLane > 0 ? kWordsPerLane * kElemsPerWord : 1;
 
   // grad_out values of the words this lane scatters.

@@ -65,10 +65,13 @@ def test_fused_matches_float64_oracle(case, dtype, per_level):
     check(out, grads, ref_out, ref_grads, dtype)
 
 
+@pytest.mark.parametrize("priv", ["1", "0"], ids=["dedup", "direct"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
-def test_fused_direct_backward_kernel(dtype, monkeypatch):
-    """The direct (non-dedup) backward kernel in its fused variant."""
-    monkeypatch.setenv("MSDA_BWD_PRIV", "0")
+def test_fused_atomic_backward_kernels(dtype, priv, monkeypatch):
+    """The atomic backward kernels (row-dedup and direct) in their fused
+    variants; the default for these sizes is the owner-computes backward."""
+    monkeypatch.setenv("MSDA_BWD_OWNER", "0")
+    monkeypatch.setenv("MSDA_BWD_PRIV", priv)
     case = FUSED_CASES[0]
     value, shapes, starts, ref, off, logits = make_fused_inputs(
         **kw(case), dtype=dtype, device=DEVICE, per_level=True)

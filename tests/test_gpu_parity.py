@@ -199,10 +199,12 @@ def test_backward_loc_and_attn_grads_are_deterministic():
 # ---------------------------------------------------------------------------
 
 OVERRIDES = [
-    dict(),                                          # defaults: dedup backward
-    dict(MSDA_BWD_PRIV="0"),                         # direct backward, 16 lanes/row
-    dict(MSDA_BWD_PRIV="0", MSDA_BWD_CB="16", MSDA_BWD_TS="4"),
-    dict(MSDA_BWD_PRIV="0", MSDA_BWD_CB="8", MSDA_BWD_TS="16"),
+    dict(),                                          # defaults: owner backward
+    dict(MSDA_BWD_OWNER="0"),                        # atomic row-dedup backward
+    dict(MSDA_BWD_OWNER="0", MSDA_BWD_PRIV="0"),     # direct backward, 16 lanes/row
+    dict(MSDA_BWD_OWNER="0", MSDA_BWD_PRIV="0", MSDA_BWD_CB="16", MSDA_BWD_TS="4"),
+    dict(MSDA_BWD_OWNER="0", MSDA_BWD_PRIV="0", MSDA_BWD_CB="8", MSDA_BWD_TS="16"),
+    dict(MSDA_FWD_TS="1", MSDA_FWD_CB="8"),          # owner path, other dot-kernel shapes
     dict(MSDA_FWD_TS="1"), dict(MSDA_FWD_TS="16"),
     dict(MSDA_FWD_CB="8", MSDA_FWD_TS="4"), dict(MSDA_FWD_CB="4", MSDA_FWD_TS="2"),
 ]
