@@ -218,7 +218,7 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
 #pragma unroll
   for (int k = 0; k < kGIt; ++k) {
     const int kk = tid + k * kBlock;
-    const int q = kk / p.g_real;
+    const int q = (int)fdiv((uint32_t)kk, p.div_g);
     const uint32_t off = kk < nchunk ? gq0 + (uint32_t)q * gqs + (uint32_t)(kk - q * p.g_real) * 16u
                                      : 0x80000000u;
     graw[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0);
@@ -244,28 +244,31 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
   const OwnRsrc rs = {make_rsrc(p.loc, nsp * 2u * e), make_rsrc(p.attn, nsp * e),
                       make_rsrc(p.ref, FUSED ? p.ref_bytes : 0u),
                       make_rsrc(p.lse, FUSED ? (uint32_t)p.npairs * 4u : 0u)};
-  char* const gval = static_cast<char*>(p.grad_acc);
-  const uint64_t row0 = (uint64_t)b * (uint32_t)p.S;  // pixel rows of batch b
-  auto row_ptr = [&](int r) {
-    return gval + ((row0 + (uint32_t)(lo + r)) * (uint32_t)p.M + m) * (uint32_t)rowb + ch * 16;
-  };
+  // Row r of the band at byte rbase + r * rstride of grad_value (32-bit
+  // buffer offsets; padding lanes get an offset past the buffer, so their
+  // stores are dropped by the range check).
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.grad_acc, p.acc_bytes);
+  const uint32_t rstride = (uint32_t)p.M * (uint32_t)rowb;
+  const uint32_t rbase =
+      live ? (((uint32_t)b * (uint32_t)p.S + (uint32_t)lo) * (uint32_t)p.M + (uint32_t)m) *
+                     (uint32_t)rowb + (uint32_t)ch * 16u
+           : 0x80000000u;
   // Store a finished row sum: plain in the first round, added to the row's
   // earlier value in later rounds (this workgroup is the row's only writer).
   auto put = [&](int r, const float (&acc)[kVec], bool written) {
-    if (!live) return;
-    char* dst = row_ptr(r);
+    const uint32_t off = rbase + (uint32_t)r * rstride;
     float v[kVec];
 #pragma unroll
     for (int k = 0; k < kVec; ++k) v[k] = acc[k];
     if (written) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(dst);
-      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+      const i32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+      const uint32_t w4[4] = {(uint32_t)raw[0], (uint32_t)raw[1], (uint32_t)raw[2], (uint32_t)raw[3]};
       float old[kVec];
       C::unpack(w4, old);
 #pragma unroll
       for (int k = 0; k < kVec; ++k) v[k] += old[k];
     }
-    C::store(dst, v);
+    __builtin_amdgcn_raw_buffer_store_b128(pack16<T>(v), rv, off, 0, 0);
   };
 
   bool written = false;
@@ -291,17 +294,21 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
     __syncthreads();  // counts zeroed (and, in later rounds, the last pieces read)
 
     // 1. Entries per row; the count an entry finds is its rank in the row.
+    // The cells (corner-00 pixel, fractions, in-band corner bits 4i..4i+3)
+    // are kept for the fill.
     uint32_t rank[NS * 2];  // 16-bit ranks, corners 2h and 2h + 1 of a sample in word h
+    int pix[NS];
+    float slx[NS], sly[NS];
+    uint32_t bits = 0;
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      int pix;
-      float lx, ly;
-      const uint32_t bits = own_cell(sx[i], sy[i], W, H, st, lo, hi, pix, lx, ly);
+      const uint32_t bi = own_cell(sx[i], sy[i], W, H, st, lo, hi, pix[i], slx[i], sly[i]);
+      bits |= bi << (4 * i);
       uint32_t rk[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         rk[c] = 0;
-        if (bits & (1u << c)) rk[c] = atomicAdd(&u.cnt[pix + (c & 1) + (c >> 1) * W - lo], 1);
+        if (bi & (1u << c)) rk[c] = atomicAdd(&u.cnt[pix[i] + (c & 1) + (c >> 1) * W - lo], 1);
       }
       rank[2 * i] = rk[0] | rk[1] << 16;
       rank[2 * i + 1] = rk[2] | rk[3] << 16;
@@ -349,17 +356,16 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
       const int r1 = a;
       const int ne = s_off[r1] - base;
 
-      // Fill: entry slot = row offset + rank.  The geometry is recomputed
-      // from (x, y, A) rather than hoisted out of the sub-band loop by the
-      // compiler: the cells and coefficients of all NS samples would
-      // otherwise stay live (~100 registers).
+      // Fill: entry slot = row offset + rank.  The per-corner values are
+      // formed here rather than hoisted out of the sub-band loop by the
+      // compiler: those of all NS samples would otherwise stay live (~100
+      // registers).
 #pragma unroll
-      for (int i = 0; i < NS; ++i) asm volatile("" : "+v"(sx[i]), "+v"(sy[i]), "+v"(sa[i]));
+      for (int i = 0; i < NS; ++i)
+        asm volatile("" : "+v"(pix[i]), "+v"(slx[i]), "+v"(sly[i]), "+v"(sa[i]));
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
-        int pix;
-        float lx, ly;
-        const uint32_t bits = own_cell(sx[i], sy[i], W, H, st, lo, hi, pix, lx, ly);
+        const float lx = slx[i], ly = sly[i];
         const uint32_t q = fdiv((uint32_t)min(tid + i * kBlock, nsmp - 1), p.div_k);
         const float mx = 1.f - lx, my = 1.f - ly;
         // The four row offsets are read unconditionally (row 0 stands in
@@ -368,8 +374,8 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
         bool in[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          r[c] = pix + (c & 1) + (c >> 1) * W - lo;
-          in[c] = (bits & (1u << c)) && r[c] >= r0 && r[c] < r1;
+          r[c] = pix[i] + (c & 1) + (c >> 1) * W - lo;
+          in[c] = (bits & (1u << (4 * i + c))) && r[c] >= r0 && r[c] < r1;
           o[c] = s_off[in[c] ? r[c] : 0];
         }
 #pragma unroll
@@ -450,6 +456,7 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
       __syncthreads();
       if (tail_row >= 0) {  // add the pieces of the later slices, in order
         const int t2 = (s_off[tail_row + 1] - base - 1) / cs;
+#pragma unroll 4
         for (int t = team + 1; t <= t2; ++t) {
 #pragma unroll
           for (int k = 0; k < kVec; ++k) acc[k] += u.piece[(t * G + ch) * kVec + k];

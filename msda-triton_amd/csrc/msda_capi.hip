@@ -310,6 +310,7 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
         po.g_real = own.g_real;
         po.g_rt = own.g_rt;
         po.own_lg = own.own_lg;
+        po.div_g = make_fastdiv((uint32_t)own.g_real);
         if (f) po.ref_bytes = (uint32_t)(nb * ref_per_b * e);
         rc = status(launch_owner(dtype, f != nullptr, po, st));
         if (rc != MSDA_OK) return rc;

@@ -175,6 +175,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
                                            kRsrcWord3);
 }
 
+// 16 bytes of T from 16 / elem floats (round to nearest even), as the four
+// dwords of a 128-bit store.
+template <class T>
+__device__ __forceinline__ i32x4 pack16(const float (&v)[16 / T::kBytes]) {
+  i32x4 w;
+  if constexpr (T::kBytes == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = __float_as_int(v[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = (int)pack2<T>(v[2 * i], v[2 * i + 1]);
+  }
+  return w;
+}
+
 // --------------------------------------------------------------------------
 // Chunk = CB contiguous bytes of one value row, VEC = CB / elem floats.
 // --------------------------------------------------------------------------
@@ -354,6 +369,7 @@ struct Params {
   int32_t own_split;   //   least bands per level (entry balance)
   int32_t own_groups;  //   bands (workgroups) per (b, m) in the grid
   int32_t own_lg;      //   log2 of the lanes per row (g_rt)
+  FastDiv div_g;       //   division by g_real (live lanes per row)
   uint32_t ref_bytes;  //   fused: num_records of the reference points
   FastDiv div_qm, div_m, div_k, div_d;
 };
