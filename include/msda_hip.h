@@ -79,20 +79,30 @@ int msda_forward(const void* value, const int64_t* spatial_shapes,
  *
  * Replaces src/msda_triton/ops.py:76-92 and the kernel
  * src/msda_triton/kernels.py:166-291.
- *   grad_value              (B, S, M, D) dtype, written in full (the library
- *                           zero-fills it on `stream`; the caller need not).
- *   grad_value_accum        NULL: grad_value is accumulated in place with the
- *                           dtype's own atomics (fp32 add, packed fp16/bf16
- *                           add).  Non-NULL: an fp32 scratch array of B*S*M*D
- *                           floats; gradients are accumulated there with fp32
- *                           atomics and rounded once into grad_value.  This
- *                           is the reference's `fp32_grad_accum=True`
+ *   grad_value              (B, S, M, D) dtype, written in full; its contents
+ *                           on entry do not matter.
+ *   grad_value_accum        NULL: on the atomic paths grad_value is
+ *                           accumulated in place with the dtype's own atomics
+ *                           (fp32 add, packed fp16/bf16 add).  Non-NULL: an
+ *                           fp32 scratch array of B*S*M*D floats; the atomic
+ *                           paths accumulate there with fp32 atomics and
+ *                           round once into grad_value.  This is the
+ *                           reference's `fp32_grad_accum=True`
  *                           (src/msda_triton/ops.py:76-77,91-92).  For
  *                           dtype == MSDA_DTYPE_F32 it may alias grad_value.
  *   grad_sampling_locations (B, Q, M, L, K, 2) dtype, written in full.
  *   grad_attention_weights  (B, Q, M, L, K)    dtype, written in full.
- * grad_value is accumulated with atomics, so it is not bitwise
- * deterministic; the other two gradients are.
+ * The library picks one of three ways to form grad_value
+ * (msda_backward_plan reports which): for few samples per (batch, head,
+ * level) -- Q*K <= 2048, a head row of a multiple of 16 bytes up to 256,
+ * Q*D*elem <= 20480, 16-byte aligned grad_output and grad_value -- workgroups
+ * that own bands of value rows sum each element's contributions in fp32 and
+ * store it once (no atomics, no zero-fill, grad_value_accum unused);
+ * otherwise grad_value is zero-filled on `stream` and accumulated with
+ * atomics, by a kernel that merges samples sharing a row within a workgroup
+ * or, for shapes it does not cover, by the direct scatter.  grad_value is
+ * not bitwise deterministic on any of them (the summation order varies);
+ * the other two gradients are.
  */
 int msda_backward(const void* value, const int64_t* spatial_shapes,
                   const int64_t* level_start_index, const void* sampling_locations,
@@ -261,6 +271,24 @@ const char* msda_error_string(int code);
 
 /* Library ABI version, (major << 16) | minor. */
 int msda_abi_version(void);
+
+/*
+ * Which way msda_backward / msda_fused_backward (deterministic == 0) or their
+ * deterministic variants (deterministic != 0) form grad_value for these
+ * sizes, assuming 16-byte aligned grad_output and grad_value: one of the
+ * MSDA_BACKWARD_* codes below, or minus an MSDA_ERR_* code for sizes or a
+ * dtype the backward rejects.  Host-only (no device work); it reads the
+ * same MSDA_BWD_OWNER / MSDA_BWD_PRIV overrides as the backward.  No
+ * counterpart in the reference, whose backward has a single kernel
+ * (src/msda_triton/ops.py:76-92): it serves callers and benchmarks that
+ * report which kernels ran.
+ */
+#define MSDA_BACKWARD_ATOMIC_DIRECT 0 /* zero-fill + direct atomic scatter */
+#define MSDA_BACKWARD_ATOMIC_DEDUP 1  /* zero-fill + row-merging atomic kernel */
+#define MSDA_BACKWARD_OWNER 2         /* row-owner kernel + scatter-free gradient kernel */
+int msda_backward_plan(int64_t batch, int64_t num_keys, int64_t num_heads, int64_t head_dim,
+                       int64_t num_queries, int64_t num_levels, int64_t num_points, int dtype,
+                       int deterministic);
 
 #ifdef __cplusplus
 }

@@ -647,4 +647,26 @@ extern "C" const char* msda_error_string(int code) {
   }
 }
 
-extern "C" int msda_abi_version(void) { return (1 << 16) | 3; }
+extern "C" int msda_abi_version(void) { return (1 << 16) | 4; }
+
+extern "C" int msda_backward_plan(int64_t batch, int64_t num_keys, int64_t num_heads,
+                                  int64_t head_dim, int64_t num_queries, int64_t num_levels,
+                                  int64_t num_points, int dtype, int deterministic) {
+  const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
+  const int rc = check_dims(d, dtype);
+  if (rc != MSDA_OK) return -rc;
+  const int e = elem_bytes(dtype);
+  const bool compute = d.B * d.Q * d.M * d.L * d.K > 0 && d.B * d.Q * d.M * d.D > 0 && d.S > 0;
+  Params own = {};
+  base_params(d, 0, d.B, dtype, &own);
+  if (compute && !deterministic && bwd_owner_enabled() &&
+      owner_plan(d.Q, d.K, d.D, d.S, d.L, e, &own))
+    return MSDA_BACKWARD_OWNER;
+  Shape sh;
+  if (compute && !choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, true,
+                               bwd_ts_pref(), bwd_cb_pref(), &sh))
+    return -MSDA_ERR_UNSUPPORTED_SHAPE;
+  if (compute && bwd_priv_enabled() && priv_supported(sh, (int)d.D, (int)d.K, e))
+    return MSDA_BACKWARD_ATOMIC_DEDUP;
+  return MSDA_BACKWARD_ATOMIC_DIRECT;
+}

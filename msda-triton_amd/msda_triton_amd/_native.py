@@ -40,6 +40,7 @@ SIGNATURES = {
     "msda_projection_backward": (_INT, [_P] * 12 + [_I64] * 4 + [_INT, _P]),
     "msda_error_string": (ctypes.c_char_p, [_INT]),
     "msda_abi_version": (_INT, []),
+    "msda_backward_plan": (_INT, [_I64] * 7 + [_INT, _INT]),
 }
 
 _lock = threading.Lock()

@@ -15,11 +15,21 @@ import pytest
 import torch
 
 from msda_cases import BWD_RELERR, BWD_TOL, DTYPES, make_inputs, rel_err
+from msda_triton_amd import _native
 from msda_triton_amd import multi_scale_deformable_attention as msda
 from oracle import msda_backward_analytic, run_reference_fp32
 
 pytestmark = pytest.mark.gpu
 DEVICE = "cuda"
+OWNER, DEDUP = 2, 1
+DCODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+
+def plan(value, loc):
+    """grad_value path the library takes for these inputs (msda_backward_plan)."""
+    B, S, M, D = value.shape
+    _, Q, _, L, K, _ = loc.shape
+    return _native.load().msda_backward_plan(B, S, M, D, Q, L, K, DCODE[value.dtype], 0)
 
 
 def check_grads(grads, refs, dtype):
@@ -51,6 +61,8 @@ def test_decoder_shapes_both_paths(dtype, owner, monkeypatch):
     value, shapes, starts, loc, attn = make_inputs(
         B=2, Q=300, M=4, D=32, shapes=[(50, 84), (25, 42), (13, 21), (7, 11)], K=4,
         dtype=dtype, device=DEVICE, loc_lo=-0.1, loc_hi=1.1)
+    expect = OWNER if owner == "1" and dtype != torch.float32 else DEDUP  # fp32: 38 KB of grad_out
+    assert plan(value, loc) == expect
     g, grads = fwd_bwd(value, shapes, starts, loc, attn)
     _, refs = run_reference_fp32(value, shapes, loc, attn, g)
     check_grads(grads, refs, dtype)
@@ -65,17 +77,21 @@ def test_row_widths(D, dtype):
     value, shapes, starts, loc, attn = make_inputs(
         B=2, Q=40, M=3, D=D, shapes=[(9, 13), (5, 7)], K=3, dtype=dtype, device=DEVICE,
         loc_lo=-0.2, loc_hi=1.2)
+    row = D * value.element_size()
+    assert (plan(value, loc) == OWNER) == (row % 16 == 0 and row <= 256)
     g, grads = fwd_bwd(value, shapes, starts, loc, attn)
     _, refs = run_reference_fp32(value, shapes, loc, attn, g)
     check_grads(grads, refs, dtype)
 
 
-@pytest.mark.parametrize("QK", [(512, 4), (513, 4)], ids=["QK2048_owner", "QK2052_atomic"])
+@pytest.mark.parametrize("QK", [(128, 16), (128, 17)], ids=["QK2048_owner", "QK2176_atomic"])
 def test_sample_count_boundary(QK):
+    """Q*K = 2048 (8 samples per lane, the owner path's limit) and beyond."""
     Q, K = QK
     value, shapes, starts, loc, attn = make_inputs(
         B=1, Q=Q, M=2, D=32, shapes=[(20, 30), (10, 15)], K=K, dtype=torch.float32,
         device=DEVICE)
+    assert plan(value, loc) == (OWNER if Q * K <= 2048 else DEDUP)
     g, grads = fwd_bwd(value, shapes, starts, loc, attn)
     _, refs = run_reference_fp32(value, shapes, loc, attn, g)
     check_grads(grads, refs, torch.float32)
@@ -87,12 +103,13 @@ def test_samples_piled_on_one_band(dtype):
     entries on a handful of rows of one band, more than one CSR pass holds,
     so the band is processed in several sub-bands."""
     value, shapes, starts, loc, attn = make_inputs(
-        B=1, Q=512, M=2, D=32, shapes=[(16, 16), (8, 8)], K=4, dtype=torch.float32,
+        B=1, Q=128, M=2, D=32, shapes=[(16, 16), (8, 8)], K=16, dtype=torch.float32,
         device="cpu")
     gen = torch.Generator().manual_seed(11)
     loc = 0.5 + 0.02 * torch.rand(loc.shape, generator=gen)
     value, loc, attn = (t.to(DEVICE, dtype) for t in (value, loc, attn))
     shapes = shapes.to(DEVICE)
+    assert plan(value, loc) == OWNER
     g, grads = fwd_bwd(value, shapes, starts.to(DEVICE), loc, attn)
     _, refs = run_reference_fp32(value, shapes, loc, attn, g)
     check_grads(grads, refs, dtype)
@@ -124,6 +141,7 @@ def test_nonstandard_level_tables(layout):
     assert all(s + n <= S for s, n in zip(starts, sizes))
     B, Q, M, D, K = 2, 60, 2, 32, 4
     gen = torch.Generator().manual_seed(5)
+    assert plan(torch.empty(B, S, M, D), torch.empty(B, Q, M, 3, K, 2)) == OWNER
     value = torch.randn(B, S, M, D, generator=gen)
     loc = -0.1 + 1.2 * torch.rand(B, Q, M, 3, K, 2, generator=gen)
     attn = torch.rand(B, Q, M, 3, K, generator=gen).flatten(3).softmax(-1).view(B, Q, M, 3, K)
@@ -166,6 +184,7 @@ def test_owner_and_atomic_paths_agree_on_decoder_preset(monkeypatch):
     from msda_triton_amd.presets import make_preset_inputs
 
     value, shapes, starts, loc, attn = make_preset_inputs("decoder", device=DEVICE)
+    assert plan(value, loc) == OWNER
     g1, grads1 = fwd_bwd(value, shapes, starts, loc, attn)
     monkeypatch.setenv("MSDA_BWD_OWNER", "0")
     g2, grads2 = fwd_bwd(value, shapes, starts, loc, attn, fp32_grad_accum=True)

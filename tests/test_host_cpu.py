@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_strings(lib):
-    assert lib.msda_abi_version() == (1 << 16) | 3
+    assert lib.msda_abi_version() == (1 << 16) | 4
     for code in range(5):
         assert lib.msda_error_string(code)
     assert b"unknown" in lib.msda_error_string(99)
@@ -208,6 +208,35 @@ def test_custom_ops_are_registered_with_fake_shapes():
         grads = torch.ops.msda_amd.fused_backward(value, shapes, starts, ref, loc, attn, lse, out,
                                                   g, False, 1, True)
         assert [t.shape for t in grads] == [value.shape, ref.shape, loc.shape, attn.shape]
+
+
+def test_backward_plan(lib, monkeypatch):
+    """Which grad_value path each preset's shapes take (host-only query)."""
+    owner, dedup, direct = 2, 1, 0
+    # decoder (B4 Q300 L4 K4, bf16): Q*K = 1200 per level, 64-byte rows
+    assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 0) == owner
+    assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 1) == dedup  # deterministic
+    # encoder / Mask2Former: Q = S, far more samples per (b, m, level)
+    assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 0) == dedup
+    assert lib.msda_backward_plan(2, 21504, 8, 32, 21504, 3, 4, 0, 0) == dedup
+    # limits of the owner path: Q*K <= 2048, Q*D*elem <= 20480, rows of 16..256 bytes
+    assert lib.msda_backward_plan(1, 600, 2, 32, 128, 2, 16, 1, 0) == owner  # Q*K = 2048
+    assert lib.msda_backward_plan(1, 600, 2, 32, 128, 2, 17, 1, 0) == dedup
+    assert lib.msda_backward_plan(1, 600, 2, 32, 320, 2, 4, 1, 0) == owner   # 20480 B
+    assert lib.msda_backward_plan(1, 600, 2, 32, 321, 2, 4, 1, 0) == dedup
+    assert lib.msda_backward_plan(1, 600, 2, 32, 160, 2, 4, 0, 0) == owner   # 20480 B
+    assert lib.msda_backward_plan(1, 600, 2, 32, 161, 2, 4, 0, 0) == dedup
+    assert lib.msda_backward_plan(1, 600, 2, 3, 100, 2, 4, 1, 0) == direct   # odd half row
+    assert lib.msda_backward_plan(1, 600, 2, 128, 40, 2, 4, 1, 0) == owner   # 256-byte rows
+    assert lib.msda_backward_plan(1, 600, 2, 256, 40, 2, 4, 1, 0) != owner
+    # overrides read per call
+    monkeypatch.setenv("MSDA_BWD_OWNER", "0")
+    assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 0) == dedup
+    monkeypatch.setenv("MSDA_BWD_PRIV", "0")
+    assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 0) == direct
+    # errors come back negated
+    assert lib.msda_backward_plan(1, 1, 1, 1, 1, 1, 1, 9, 0) == -2
+    assert lib.msda_backward_plan(-1, 1, 1, 1, 1, 1, 1, 0, 0) == -1
 
 
 def test_deterministic_workspace_size(lib):
