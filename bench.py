@@ -15,7 +15,8 @@ Prints ONE JSON line:
                accounting, labs/03_the_machine.py:232-251)
   ms_per_step  fwd+bwd wall time per step over the K timed steps
   fwd_us / bwd_us / fwd_gbps ...  per-call device times from HIP events around
-               graph replays of R calls (bwd = zero-fill + backward kernel);
+               graph replays of R calls (bwd = every kernel of one msda_backward
+               call: owner + gradient kernels, or zero-fill + atomic kernel);
                *_cold_us with L2 and Infinity Cache flushed before each call;
                bwd_deterministic_us the bitwise-reproducible backward
   roofline     backward pass (the dominant cost) vs 8 TB/s HBM
@@ -46,6 +47,14 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "msda-triton_amd"))
 
 HBM_PEAK_GBPS = 8000.0
+
+# msda_backward_plan codes -> the kernels one msda_backward call runs.
+BACKWARD_KERNELS = {
+    0: "msda_backward call (zero-fill + direct atomic bwd_kernel)",
+    1: "msda_backward call (zero-fill + row-dedup atomic bwd_priv_kernel)",
+    2: "msda_backward call (owner_kernel for grad_value + bwd_kernel without scatter for "
+       "grad_loc/grad_attn)",
+}
 
 
 def _cpu_model() -> str:
@@ -604,7 +613,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(bwd_gbps / HBM_PEAK_GBPS, 4),
             "traffic": _traffic(args.preset, "backward"),
-            "kernel": "msda_backward call (zero-fill + row-dedup bwd_priv_kernel)",
+            "kernel": BACKWARD_KERNELS.get(
+                lib.msda_backward_plan(*dims, dt, 0), "msda_backward call"),
             "algorithmic_bytes": bwd_b,
         },
         "roofline_fwd": {
