@@ -215,7 +215,8 @@ def deterministic_backward(lib, value, shapes, starts, loc, attn, grad_out):
     def call():
         _native.check(lib.msda_backward_deterministic(
             value.data_ptr(), shapes.data_ptr(), starts.data_ptr(), loc.data_ptr(),
-            attn.data_ptr(), grad_out.data_ptr(), gv.data_ptr(), ws.data_ptr(), gl.data_ptr(),
+            attn.data_ptr(), grad_out.data_ptr(), gv.data_ptr(),
+            None if ws is None else ws.data_ptr(), gl.data_ptr(),
             ga.data_ptr(), B, S, M, D, Q, L, K, dt, torch.cuda.current_stream().cuda_stream),
             "msda_backward_deterministic")
 

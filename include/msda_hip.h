@@ -100,9 +100,11 @@ int msda_forward(const void* value, const int64_t* spatial_shapes,
  * store it once (no atomics, no zero-fill, grad_value_accum unused);
  * otherwise grad_value is zero-filled on `stream` and accumulated with
  * atomics, by a kernel that merges samples sharing a row within a workgroup
- * or, for shapes it does not cover, by the direct scatter.  grad_value is
- * not bitwise deterministic on any of them (the summation order varies);
- * the other two gradients are.
+ * or, for shapes it does not cover, by the direct scatter.  On the owner
+ * path grad_value is bitwise reproducible (each element one fp32 sum in an
+ * order fixed by the inputs); on the atomic paths it is not (the order of
+ * the atomics varies).  The other two gradients are reproducible on every
+ * path.
  */
 int msda_backward(const void* value, const int64_t* spatial_shapes,
                   const int64_t* level_start_index, const void* sampling_locations,
@@ -172,17 +174,23 @@ int msda_fused_backward(const void* value, const int64_t* spatial_shapes,
  * Deterministic backward.  The reference accumulates grad_value with
  * floating-point atomics, so its sums depend on their arrival order and are
  * not reproducible bit for bit (documented at src/msda_triton/ops.py:135-138).
- * These variants accumulate it in int64 fixed point instead: each
- * contribution c is added as round(c * 2^e), integer addition is exact, and
- * the result is identical on every run.  e is chosen per call from
- * Q*L*K * max|A| * max|grad_output| (a bound on every element) so that no
- * sum can overflow; the resolution, that bound times 2^-60, is far below
- * fp32 rounding.  grad_sampling_locations / grad_attention_weights (and the
- * fused gradients) are deterministic in every variant.
+ * These variants make it identical on every run.  Calls that take the owner
+ * path (msda_backward_plan(..., 1) == MSDA_BACKWARD_OWNER; see msda_backward)
+ * get it from there: every element is one fp32 sum over its contributions
+ * in an order fixed by the inputs, no workspace needed.  Other calls
+ * accumulate in int64 fixed point: each contribution c is added as
+ * round(c * 2^e), integer addition is exact, and the result does not depend
+ * on the order.  e is chosen per call from Q*L*K * max|A| *
+ * max|grad_output| (a bound on every element) so that no sum can overflow;
+ * the resolution, that bound times 2^-60, is far below fp32 rounding.
+ * grad_sampling_locations / grad_attention_weights (and the fused
+ * gradients) are deterministic in every variant.
  *
  *   workspace   device scratch of msda_deterministic_workspace_bytes(B, S, M,
  *               D, Q, L, K, dtype) bytes (the int64 accumulator plus the scale
- *               words; -1 for invalid sizes or dtype); its contents on entry
+ *               words; 0 when the call takes the owner path, given 16-byte
+ *               aligned grad_output and grad_value -- workspace may then be
+ *               NULL; -1 for invalid sizes or dtype); its contents on entry
  *               do not matter.
  * Other arguments as in msda_backward / msda_fused_backward (no fp32
  * accumulator: the integer accumulator replaces it).

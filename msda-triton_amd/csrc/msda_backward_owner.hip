@@ -181,11 +181,12 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
 
   __shared__ LevelTable lt;
   __shared__ uint16_t s_off[kOwnRows + 1];  // CSR offsets (exclusive prefix sum of the counts)
-  // Entries per row (count pass); then the CSR entries (A * w_c, query |
+  // Entries per row counted per wave (count pass), then each wave's
+  // exclusive prefix over the waves; then the CSR entries (A * w_c, query |
   // local row << kOwnQBits), rows contiguous; then, after the entries are
   // read, each team's piece of the row it continues from the slice before.
   __shared__ union {
-    int cnt[kOwnRows];
+    int cnt[kBlock / kWave][kOwnRows];
     float2 csr[kOwnCap];
     float piece[kBlock * kVec];
   } u;
@@ -290,12 +291,18 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
       own_sample<T, FUSED>(p, rs, bq * (uint32_t)p.M + m, (uint32_t)(l * p.K + j) - q * p.K, bq,
                            (uint32_t)l, valid, fw, fh, sx[i], sy[i], sa[i]);
     }
-    for (int r = tid; r < nrows; r += kBlock) u.cnt[r] = 0;
+#pragma unroll
+    for (int w = 0; w < kBlock / kWave; ++w)
+      for (int r = tid; r < nrows; r += kBlock) u.cnt[w][r] = 0;
     __syncthreads();  // counts zeroed (and, in later rounds, the last pieces read)
 
-    // 1. Entries per row; the count an entry finds is its rank in the row.
-    // The cells (corner-00 pixel, fractions, in-band corner bits 4i..4i+3)
-    // are kept for the fill.
+    // 1. Entries per row.  Each wave counts into its own counters, so the
+    // count an entry finds -- its rank among the wave's entries of the row
+    // -- depends only on that wave's instructions, in program order; the
+    // ranks (and so the CSR order and every row sum) are the same on every
+    // run.  The cells (corner-00 pixel, fractions, in-band corner bits
+    // 4i..4i+3) are kept for the fill.
+    const int wave = tid / kWave;
     uint32_t rank[NS * 2];  // 16-bit ranks, corners 2h and 2h + 1 of a sample in word h
     int pix[NS];
     float slx[NS], sly[NS];
@@ -308,20 +315,30 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         rk[c] = 0;
-        if (bi & (1u << c)) rk[c] = atomicAdd(&u.cnt[pix[i] + (c & 1) + (c >> 1) * W - lo], 1);
+        if (bi & (1u << c))
+          rk[c] = atomicAdd(&u.cnt[wave][pix[i] + (c & 1) + (c >> 1) * W - lo], 1);
       }
       rank[2 * i] = rk[0] | rk[1] << 16;
       rank[2 * i + 1] = rk[2] | rk[3] << 16;
     }
     __syncthreads();
 
-    // 2. CSR offsets.
+    // 2. CSR offsets of the rows' totals; each wave's counter becomes the
+    // sum over the waves before it.
     {
       int c4[4], sum = 0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int r = tid * 4 + k;
-        c4[k] = r < nrows ? u.cnt[r] : 0;
+        c4[k] = 0;
+        if (r < nrows) {
+#pragma unroll
+          for (int w = 0; w < kBlock / kWave; ++w) {
+            const int n = u.cnt[w][r];
+            u.cnt[w][r] = c4[k];
+            c4[k] += n;
+          }
+        }
         sum += c4[k];
       }
       int tot;
@@ -334,7 +351,23 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
       }
       if (tid == 0) s_off[nrows] = (uint16_t)tot;
     }
-    __syncthreads();  // offsets written, counts dead (the CSR reuses them)
+    __syncthreads();
+
+    // An entry's rank in its row: the entries of the waves before it, then
+    // its rank within its wave.
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      int before[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const bool in = (bits >> (4 * i + c)) & 1u;
+        before[c] = u.cnt[wave][in ? pix[i] + (c & 1) + (c >> 1) * W - lo : 0];
+        if (!in) before[c] = 0;
+      }
+      rank[2 * i] += (uint32_t)before[0] | (uint32_t)before[1] << 16;
+      rank[2 * i + 1] += (uint32_t)before[2] | (uint32_t)before[3] << 16;
+    }
+    __syncthreads();  // counters read: the CSR reuses them
 
     // 3. Sub-bands of at most kOwnCap entries: one unless many samples pile
     // onto the band.  A row alone never exceeds it: a sample puts at most one

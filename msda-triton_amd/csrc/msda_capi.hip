@@ -210,14 +210,15 @@ static int forward_impl(const void* value, const int64_t* spatial_shapes,
   return MSDA_OK;
 }
 
-// det_workspace != NULL selects the deterministic backward: grad_value is
-// accumulated there as int64 fixed point (n_val * 8 bytes) followed by the
-// two max words of the scale (det_scale).
+// deterministic: bitwise-reproducible grad_value -- the owner path where it
+// applies, else int64 fixed-point accumulation in det_workspace (n_val * 8
+// bytes followed by the two max words of the scale, det_scale).
 static int backward_impl(const void* value, const int64_t* spatial_shapes,
                          const int64_t* level_start_index, const void* loc, const void* attn,
                          const void* grad_output, void* grad_value, float* grad_value_accum,
                          void* grad_loc, void* grad_attn, const Dims& d, int dtype, void* stream,
-                         const FusedArgs* f, void* det_workspace = nullptr) {
+                         const FusedArgs* f, bool deterministic = false,
+                         void* det_workspace = nullptr) {
   int rc = check_dims(d, dtype);
   if (rc != MSDA_OK) return rc;
   const int e = elem_bytes(dtype);
@@ -231,15 +232,17 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
   if (f && n_smp > 0 && n_out > 0 && d.S > 0 && (!f->ref || !f->lse || !f->output))
     return MSDA_ERR_INVALID_ARGUMENT;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool det = det_workspace != nullptr && n_val > 0;
   const bool compute = n_smp > 0 && n_out > 0 && d.S > 0;
   // Owner-computes grad_value (few samples per (b, m, level)): every element
-  // stored once in fp32-accumulated form, so neither the zero-fill nor the
-  // fp32 scratch is used.
+  // stored once from an fp32 sum in a fixed order -- bitwise reproducible,
+  // so it also serves the deterministic entry points -- and neither the
+  // zero-fill, the fp32 scratch nor the deterministic workspace is used.
   Params own = {};
   base_params(d, 0, d.B, dtype, &own);
-  const bool owner = compute && !det && bwd_owner_enabled() && aligned16(grad_output) &&
+  const bool owner = compute && bwd_owner_enabled() && aligned16(grad_output) &&
                      aligned16(grad_value) && owner_plan(d.Q, d.K, d.D, d.S, d.L, e, &own);
+  if (deterministic && !owner && !det_workspace && n_val > 0) return MSDA_ERR_INVALID_ARGUMENT;
+  const bool det = deterministic && !owner && n_val > 0;
   // fp32 accumulation is only a separate path for half storage.
   const bool fp32_acc =
       !owner && !det && grad_value_accum != nullptr && dtype != kF32 && n_val > 0;
@@ -431,6 +434,10 @@ extern "C" int64_t msda_deterministic_workspace_bytes(int64_t batch, int64_t num
                                                       int64_t num_points, int dtype) {
   const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
   if (check_dims(d, dtype) != MSDA_OK) return -1;
+  // None on the owner path (16-byte aligned grad_output / grad_value assumed).
+  if (msda_backward_plan(batch, num_keys, num_heads, head_dim, num_queries, num_levels,
+                         num_points, dtype, 1) == MSDA_BACKWARD_OWNER)
+    return 0;
   return batch * num_keys * num_heads * head_dim * 8 + 64;
 }
 
@@ -442,11 +449,10 @@ extern "C" int msda_backward_deterministic(
     int64_t head_dim, int64_t num_queries, int64_t num_levels, int64_t num_points, int dtype,
     void* stream) {
   const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
-  if (!workspace && batch * num_keys * num_heads * head_dim > 0) return MSDA_ERR_INVALID_ARGUMENT;
   return backward_impl(value, spatial_shapes, level_start_index, sampling_locations,
                        attention_weights, grad_output, grad_value, nullptr,
                        grad_sampling_locations, grad_attention_weights, d, dtype, stream, nullptr,
-                       workspace);
+                       true, workspace);
 }
 
 extern "C" int msda_fused_backward_deterministic(
@@ -459,12 +465,11 @@ extern "C" int msda_fused_backward_deterministic(
     int reference_levels, int dtype, void* stream) {
   if (reference_levels != 0 && reference_levels != 1) return MSDA_ERR_INVALID_ARGUMENT;
   const Dims d{batch, num_keys, num_heads, head_dim, num_queries, num_levels, num_points};
-  if (!workspace && batch * num_keys * num_heads * head_dim > 0) return MSDA_ERR_INVALID_ARGUMENT;
   const FusedArgs f{reference_points, const_cast<float*>(softmax_lse), output,
                     grad_reference_points, reference_levels};
   return backward_impl(value, spatial_shapes, level_start_index, sampling_offsets,
                        attention_logits, grad_output, grad_value, nullptr, grad_sampling_offsets,
-                       grad_attention_logits, d, dtype, stream, &f, workspace);
+                       grad_attention_logits, d, dtype, stream, &f, true, workspace);
 }
 
 // ---------------------------------------------------------------------------
@@ -659,8 +664,8 @@ extern "C" int msda_backward_plan(int64_t batch, int64_t num_keys, int64_t num_h
   const bool compute = d.B * d.Q * d.M * d.L * d.K > 0 && d.B * d.Q * d.M * d.D > 0 && d.S > 0;
   Params own = {};
   base_params(d, 0, d.B, dtype, &own);
-  if (compute && !deterministic && bwd_owner_enabled() &&
-      owner_plan(d.Q, d.K, d.D, d.S, d.L, e, &own))
+  (void)deterministic;  // the owner path serves both modes
+  if (compute && bwd_owner_enabled() && owner_plan(d.Q, d.K, d.D, d.S, d.L, e, &own))
     return MSDA_BACKWARD_OWNER;
   Shape sh;
   if (compute && !choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, true,

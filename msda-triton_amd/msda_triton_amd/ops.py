@@ -38,22 +38,25 @@ def _use_fp32_grad_accum(value: torch.Tensor) -> bool:
 
 def _use_deterministic(deterministic: bool | None) -> bool:
     """``None`` follows ``torch.use_deterministic_algorithms``: grad_value is
-    then accumulated in int64 fixed point, which makes it bitwise
-    reproducible (the other gradients always are)."""
+    then bitwise reproducible (the other gradients always are)."""
     if deterministic is None:
         return torch.are_deterministic_algorithms_enabled()
     return bool(deterministic)
 
 
-def deterministic_workspace(value: torch.Tensor, sampling_locations: torch.Tensor) -> torch.Tensor:
-    """Scratch of the deterministic backward (binned entries, or an int64
-    accumulator), sized by the library for this shape."""
+def deterministic_workspace(value: torch.Tensor,
+                            sampling_locations: torch.Tensor) -> torch.Tensor | None:
+    """Scratch of the deterministic backward (the int64 accumulator), sized
+    by the library for this shape; None when the call takes the owner path,
+    which is reproducible without one."""
     B, S, M, D = value.shape
     _, Q, _, L, K, _ = sampling_locations.shape
     nbytes = _native.load().msda_deterministic_workspace_bytes(B, S, M, D, Q, L, K,
                                                                _DTYPE_CODE[value.dtype])
     if nbytes < 0:
         raise ValueError("unsupported shape or dtype for the deterministic backward")
+    if nbytes == 0:
+        return None
     return torch.empty(nbytes, dtype=torch.uint8, device=value.device)
 
 
@@ -199,8 +202,9 @@ def multi_scale_deformable_attention(
         fp32_grad_accum: accumulate ``grad_value`` in an fp32 scratch buffer
             (rounded once to the value dtype) instead of native-dtype atomics.
             ``None`` selects the native atomics (see ``_use_fp32_grad_accum``).
-        deterministic: accumulate ``grad_value`` in int64 fixed point (exact
-            sums, bitwise reproducible; slower).  ``None`` follows
+        deterministic: make ``grad_value`` bitwise reproducible (decoder-style
+            calls are on their default path; others accumulate in int64
+            fixed point, exact sums, slower).  ``None`` follows
             ``torch.are_deterministic_algorithms_enabled()``.  Overrides
             ``fp32_grad_accum``.  Not in the reference's signature (keyword
             only, so calls written for the reference are unaffected).
@@ -209,9 +213,10 @@ def multi_scale_deformable_attention(
         ``(B, Q, M * D)`` output, same dtype as ``value``.
 
     Note:
-        By default ``grad_value`` is accumulated with floating-point atomics,
+        By default ``grad_value`` of encoder-style calls (many samples per
+        batch, head and level) is accumulated with floating-point atomics,
         so it is not bitwise deterministic (as in the reference); see
-        ``deterministic``.
+        ``deterministic``.  Decoder-style calls are reproducible either way.
     """
     prep = _prepare(value, spatial_shapes, level_start_index, sampling_locations,
                     attention_weights, fp32_grad_accum, deterministic)

@@ -215,7 +215,8 @@ def test_backward_plan(lib, monkeypatch):
     owner, dedup, direct = 2, 1, 0
     # decoder (B4 Q300 L4 K4, bf16): Q*K = 1200 per level, 64-byte rows
     assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 0) == owner
-    assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 1) == dedup  # deterministic
+    assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 1) == owner  # deterministic
+    assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 1) == dedup
     # encoder / Mask2Former: Q = S, far more samples per (b, m, level)
     assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 0) == dedup
     assert lib.msda_backward_plan(2, 21504, 8, 32, 21504, 3, 4, 0, 0) == dedup
@@ -240,9 +241,11 @@ def test_backward_plan(lib, monkeypatch):
 
 
 def test_deterministic_workspace_size(lib):
-    # int64 accumulator (8 bytes per grad_value element) + the scale words.
-    assert lib.msda_deterministic_workspace_bytes(4, 22223, 8, 32, 300, 4, 4, 2) == \
-        4 * 22223 * 8 * 32 * 8 + 64
+    # int64 accumulator (8 bytes per grad_value element) + the scale words;
+    # none where the owner path (reproducible by construction) applies.
+    assert lib.msda_deterministic_workspace_bytes(2, 22223, 8, 32, 22223, 4, 4, 1) == \
+        2 * 22223 * 8 * 32 * 8 + 64
+    assert lib.msda_deterministic_workspace_bytes(4, 22223, 8, 32, 300, 4, 4, 2) == 0
     assert lib.msda_deterministic_workspace_bytes(-1, 1, 1, 1, 1, 1, 1, 0) == -1
     assert lib.msda_deterministic_workspace_bytes(1, 1, 1, 1, 1, 1, 1, 9) == -1
 
