@@ -52,8 +52,8 @@ HBM_PEAK_GBPS = 8000.0
 BACKWARD_KERNELS = {
     0: "msda_backward call (zero-fill + direct atomic bwd_kernel)",
     1: "msda_backward call (zero-fill + row-dedup atomic bwd_priv_kernel)",
-    2: "msda_backward call (owner_kernel for grad_value + bwd_kernel without scatter for "
-       "grad_loc/grad_attn)",
+    2: "msda_backward call (one owner_kernel launch: band workgroups for grad_value, then "
+       "scatter-free gradient workgroups for grad_loc/grad_attn)",
 }
 
 

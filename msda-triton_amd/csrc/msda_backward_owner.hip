@@ -35,6 +35,9 @@
 // (handled one level per round: the first round stores every row, later
 // rounds add into the rows they touch -- the workgroup is their only
 // writer) or none (rows stored as zeros).
+#include <stdlib.h>
+
+#include "msda_bwd_body.h"
 #include "msda_launch.h"
 
 namespace msda {
@@ -167,11 +170,37 @@ __device__ __forceinline__ uint32_t own_cell(float x, float y, int W, int H, int
 constexpr int kOwnQBits = 11;  // query index in a CSR entry (Q <= Q * K <= kOwnCap)
 static_assert(kOwnCap <= (1 << kOwnQBits), "query index field");
 
+// LDS of an owner workgroup.
+template <int kVec>
+struct OwnLds {
+  LevelTable lt;
+  uint16_t s_off[kOwnRows + 8];  // CSR offsets (exclusive prefix sum of the counts)
+  // Entries per row counted per wave (count pass), then each wave's
+  // exclusive prefix over the waves; then the CSR entries (A * w_c, query |
+  // local row << kOwnQBits), rows contiguous; then, after the entries are
+  // read, each team's piece of the row it continues from the slice before.
+  union {
+    int cnt[kBlock / kWave][kOwnRows];
+    float2 csr[kOwnCap];
+    float piece[kBlock * kVec];
+  } u;
+  int s_wsum[kBlock / kWave];
+  alignas(16) uint8_t s_g[kOwnGBytes];  // grad_out rows of (b, m): Q x D * elem
+};
+
 // T: storage dtype; NS: samples per lane and level (NS * kBlock >= Q * K).
 // p.g_rt lanes (a power of two, g_real of them live) cover a value row in
 // 16-byte chunks.  ~39 KB of LDS and <= 128 VGPRs: four workgroups per CU.
-template <class T, int NS, bool FUSED>
-__global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
+//
+// p.nblocks workgroups own bands of grad_value; pd.nblocks more compute
+// grad_loc / grad_attn (the direct backward body without its scatter, launch
+// shape pd).  Dispatched after the bands, they take the slots that finished
+// band workgroups free up, so the two halves of the backward overlap instead
+// of running as two launches (decoder preset: 28 us against 32 us).
+// DG > 0: the gradient workgroups' shape is 16-byte chunks, DG lanes per
+// row, 4 slots (compiled); 0: pd's runtime shape (16-byte chunks).
+template <class T, int NS, bool FUSED, int DG>
+__global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
   using C = Chunk<T, 16>;
   constexpr int kVec = C::kVec;
   constexpr int kGIt = kOwnGBytes / 16 / kBlock;  // staged 16-byte chunks per lane
@@ -179,19 +208,27 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
   static_assert(kOwnGBytes % (16 * kBlock) == 0, "whole staging rounds");
   static_assert(4 * NS * kBlock < 65536, "16-bit CSR offsets");
 
-  __shared__ LevelTable lt;
-  __shared__ uint16_t s_off[kOwnRows + 1];  // CSR offsets (exclusive prefix sum of the counts)
-  // Entries per row counted per wave (count pass), then each wave's
-  // exclusive prefix over the waves; then the CSR entries (A * w_c, query |
-  // local row << kOwnQBits), rows contiguous; then, after the entries are
-  // read, each team's piece of the row it continues from the slice before.
   __shared__ union {
-    int cnt[kBlock / kWave][kOwnRows];
-    float2 csr[kOwnCap];
-    float piece[kBlock * kVec];
-  } u;
-  __shared__ int s_wsum[kBlock / kWave];
-  __shared__ __align__(16) uint8_t s_g[kOwnGBytes];  // grad_out rows of (b, m): Q x D * elem
+    OwnLds<kVec> own;
+    BwdLds grad;
+  } smem;
+  // Chunks of 8 consecutive workgroups (one per XCD): the gradient chunks
+  // after the band chunks (p.own_mix = 0, measured fastest on the decoder,
+  // high-contention and fused cases), or before them (1).
+  const int x8 = blockIdx.x & 7, c8 = blockIdx.x >> 3;
+  const int cg = (pd.nblocks + 7) >> 3;
+  const int gc = p.own_mix ? c8 : c8 - (p.nblocks >> 3);  // gradient chunk, if in [0, cg)
+  if (gc >= 0 && gc < cg) {
+    const int blk = gc * 8 + x8;
+    if (blk < pd.nblocks)
+      bwd_body<T, NoAcc, 16, DG, DG ? 4 : 0, FUSED>(pd, xcd_remap(blk, pd.nblocks), smem.grad);
+    return;
+  }
+  LevelTable& lt = smem.own.lt;
+  uint16_t* const s_off = smem.own.s_off;
+  auto& u = smem.own.u;
+  int* const s_wsum = smem.own.s_wsum;
+  uint8_t* const s_g = smem.own.s_g;
 
   const int tid = threadIdx.x;
   // Grid: bid = 8 k + x runs on XCD x (round-robin dispatch).  Band group
@@ -199,7 +236,7 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
   // XCD (whole 128-byte lines of grad_value meet in its L2), XCDs get
   // interleaved band groups, and bands past the last level (idle groups)
   // come last in dispatch order.
-  const int x8 = blockIdx.x & 7, k8 = blockIdx.x >> 3;
+  const int k8 = p.own_mix ? c8 - cg : c8;
   const int m = k8 % p.M;
   const int bg = (k8 / p.M) * 8 + x8;
   const int nb = p.npairs / (p.Q * p.M);
@@ -511,27 +548,44 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p) {
 }
 
 template <class T, int NS, bool FUSED>
-hipError_t launch_ns(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((owner_kernel<T, NS, FUSED>), dim3(p.nblocks), dim3(kBlock), 0, st, p);
+hipError_t launch_ns(const Params& p, const Params& pd, hipStream_t st) {
+  const int grid = p.nblocks + (pd.nblocks + 7) / 8 * 8;  // p.nblocks: a multiple of 8
+  // Compiled gradient shape for 32-channel rows (2 * elem lanes of 16 bytes).
+  constexpr int kDG = 2 * T::kBytes;
+  if (pd.g_rt == kDG && pd.ts_rt == 4) {
+    hipLaunchKernelGGL((owner_kernel<T, NS, FUSED, kDG>), dim3(grid), dim3(kBlock), 0, st, p, pd);
+  } else {
+    hipLaunchKernelGGL((owner_kernel<T, NS, FUSED, 0>), dim3(grid), dim3(kBlock), 0, st, p, pd);
+  }
   return hipGetLastError();
 }
 
 template <class T, bool FUSED>
-hipError_t launch_t(const Params& p, hipStream_t st) {
+hipError_t launch_t(const Params& p, const Params& pd, hipStream_t st) {
   switch ((p.Q * p.K + kBlock - 1) / kBlock) {
-    case 1: return launch_ns<T, 1, FUSED>(p, st);
-    case 2: return launch_ns<T, 2, FUSED>(p, st);
-    case 3: return launch_ns<T, 3, FUSED>(p, st);
-    case 4: return launch_ns<T, 4, FUSED>(p, st);
-    case 5: return launch_ns<T, 5, FUSED>(p, st);
-    case 6: return launch_ns<T, 6, FUSED>(p, st);
-    case 7: return launch_ns<T, 7, FUSED>(p, st);
-    case 8: return launch_ns<T, 8, FUSED>(p, st);
+    case 1: return launch_ns<T, 1, FUSED>(p, pd, st);
+    case 2: return launch_ns<T, 2, FUSED>(p, pd, st);
+    case 3: return launch_ns<T, 3, FUSED>(p, pd, st);
+    case 4: return launch_ns<T, 4, FUSED>(p, pd, st);
+    case 5: return launch_ns<T, 5, FUSED>(p, pd, st);
+    case 6: return launch_ns<T, 6, FUSED>(p, pd, st);
+    case 7: return launch_ns<T, 7, FUSED>(p, pd, st);
+    case 8: return launch_ns<T, 8, FUSED>(p, pd, st);
     default: return hipErrorInvalidValue;
   }
 }
 
 }  // namespace
+
+// Band geometry overrides for sweeps (read per call): MSDA_OWN_ROWS, the
+// most rows per band (64..kOwnRows), and MSDA_OWN_ENTRIES, the corner
+// entries per band the level split aims at (>= 64).
+static int64_t own_env(const char* name, int64_t dflt, int64_t lo, int64_t hi) {
+  const char* v = getenv(name);
+  if (!v) return dflt;
+  const int64_t x = atoll(v);
+  return x < lo ? lo : x > hi ? hi : x;
+}
 
 bool owner_plan(int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L, int elem_bytes,
                 Params* p) {
@@ -539,10 +593,12 @@ bool owner_plan(int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L, int elem_
   if (rowb <= 0 || rowb % 16 != 0 || rowb / 16 > 16) return false;
   if (Q * K <= 0 || Q * K > kOwnCap || Q * rowb > kOwnGBytes) return false;
   if (S <= 0 || L <= 0) return false;
-  const int64_t split = (4 * Q * K + kOwnEntryTarget - 1) / kOwnEntryTarget;
-  const int64_t groups = (S + kOwnRows - 1) / kOwnRows + L * (1 + split);
+  const int64_t rows = own_env("MSDA_OWN_ROWS", kOwnRows, 64, kOwnRows);
+  const int64_t target = own_env("MSDA_OWN_ENTRIES", kOwnEntryTarget, 64, 1 << 20);
+  const int64_t split = (4 * Q * K + target - 1) / target;
+  const int64_t groups = (S + rows - 1) / rows + L * (1 + split);
   if (groups * (int64_t)p->M * 64 >= (1ll << 31)) return false;
-  p->own_rows = kOwnRows;
+  p->own_rows = (int32_t)rows;
   p->own_split = (int32_t)split;
   p->own_groups = (int32_t)groups;
   p->g_real = (int32_t)(rowb / 16);
@@ -556,16 +612,18 @@ bool owner_plan(int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L, int elem_
   return true;
 }
 
-hipError_t launch_owner(int dtype, bool fused, const Params& p0, hipStream_t st) {
+hipError_t launch_owner(int dtype, bool fused, const Params& p0, const Params& pd,
+                        hipStream_t st) {
   Params p = p0;
   const int64_t nb = p.npairs / ((int64_t)p.Q * p.M);  // batch elements in the slice
   const int64_t groups = (nb * p.own_groups + 7) / 8 * 8;  // band groups, padded to the XCDs
   p.nblocks = (int32_t)(groups * p.M);
-  if (p.nblocks == 0) return hipSuccess;
+  if (p.nblocks + pd.nblocks == 0) return hipSuccess;
   switch (dtype) {
-    case kF32: return fused ? launch_t<F32, true>(p, st) : launch_t<F32, false>(p, st);
-    case kF16: return fused ? launch_t<F16, true>(p, st) : launch_t<F16, false>(p, st);
-    case kBF16: return fused ? launch_t<BF16, true>(p, st) : launch_t<BF16, false>(p, st);
+    case kF32: return fused ? launch_t<F32, true>(p, pd, st) : launch_t<F32, false>(p, pd, st);
+    case kF16: return fused ? launch_t<F16, true>(p, pd, st) : launch_t<F16, false>(p, pd, st);
+    case kBF16:
+      return fused ? launch_t<BF16, true>(p, pd, st) : launch_t<BF16, false>(p, pd, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -314,11 +314,21 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
         po.g_rt = own.g_rt;
         po.own_lg = own.own_lg;
         po.div_g = make_fastdiv((uint32_t)own.g_real);
+        {  // sweeps: MSDA_OWN_MIX=1 gradient workgroups first, -1 two launches
+          const char* mx = getenv("MSDA_OWN_MIX");
+          po.own_mix = mx ? atoi(mx) : 0;
+        }
         if (f) po.ref_bytes = (uint32_t)(nb * ref_per_b * e);
-        rc = status(launch_owner(dtype, f != nullptr, po, st));
-        if (rc != MSDA_OK) return rc;
         finish_params(sh, kBwdRecords, &p);
-        rc = status(launch_backward(dtype, kAccNone, f != nullptr, sh, p, st));
+        // The owner launch carries the grad_loc / grad_attn workgroups when
+        // they gather 16-byte chunks (the chunk size it is compiled for);
+        // other shapes (sweep overrides) run them as a launch of their own.
+        const bool merged = sh.cb == 16 && po.own_mix >= 0;
+        Params pd = p;
+        if (!merged) pd.nblocks = 0;
+        rc = status(launch_owner(dtype, f != nullptr, po, pd, st));
+        if (rc == MSDA_OK && !merged)
+          rc = status(launch_backward(dtype, kAccNone, f != nullptr, sh, p, st));
         if (rc != MSDA_OK) return rc;
         continue;
       }

@@ -371,6 +371,7 @@ struct Params {
   int32_t own_lg;      //   log2 of the lanes per row (g_rt)
   FastDiv div_g;       //   division by g_real (live lanes per row)
   uint32_t ref_bytes;  //   fused: num_records of the reference points
+  int32_t own_mix;     //   order of band and gradient workgroups (1: gradient workgroups first, 0: last)
   FastDiv div_qm, div_m, div_k, div_d;
 };
 

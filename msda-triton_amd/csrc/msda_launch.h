@@ -52,7 +52,10 @@ hipError_t launch_backward_priv(int dtype, AccMode acc, bool fused, const Shape&
 // returns false when the call does not qualify.
 bool owner_plan(int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L, int elem_bytes,
                 Params* p);
-hipError_t launch_owner(int dtype, bool fused, const Params& p, hipStream_t st);
+// One launch: the owner workgroups (params p) followed by pd.nblocks
+// workgroups computing grad_loc / grad_attn (params pd, runtime shape).
+hipError_t launch_owner(int dtype, bool fused, const Params& p, const Params& pd,
+                        hipStream_t st);
 // Fused front-end: reference-point gradient from the offset gradients, one
 // wave per (b, q) of the nbq in the call.
 hipError_t launch_ref_grad(int dtype, const Params& p, uint64_t nbq, hipStream_t st);
