@@ -240,7 +240,7 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
   Params own = {};
   base_params(d, 0, d.B, dtype, &own);
   const bool owner = compute && bwd_owner_enabled() && aligned16(grad_output) &&
-                     aligned16(grad_value) && owner_plan(d.Q, d.K, d.D, d.S, d.L, e, &own);
+                     aligned16(grad_value) && owner_plan(d.B, d.Q, d.K, d.D, d.S, d.L, e, &own);
   if (deterministic && !owner && !det_workspace && n_val > 0) return MSDA_ERR_INVALID_ARGUMENT;
   const bool det = deterministic && !owner && n_val > 0;
   // fp32 accumulation is only a separate path for half storage.
@@ -675,7 +675,7 @@ extern "C" int msda_backward_plan(int64_t batch, int64_t num_keys, int64_t num_h
   Params own = {};
   base_params(d, 0, d.B, dtype, &own);
   (void)deterministic;  // the owner path serves both modes
-  if (compute && bwd_owner_enabled() && owner_plan(d.Q, d.K, d.D, d.S, d.L, e, &own))
+  if (compute && bwd_owner_enabled() && owner_plan(d.B, d.Q, d.K, d.D, d.S, d.L, e, &own))
     return MSDA_BACKWARD_OWNER;
   Shape sh;
   if (compute && !choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, true,

@@ -50,8 +50,8 @@ hipError_t launch_backward_priv(int dtype, AccMode acc, bool fused, const Shape&
 // once with plain stores, no atomics and no zero-fill; for calls with few
 // samples per (b, m, level).  owner_plan fills the owner fields of `p` and
 // returns false when the call does not qualify.
-bool owner_plan(int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L, int elem_bytes,
-                Params* p);
+bool owner_plan(int64_t B, int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L,
+                int elem_bytes, Params* p);
 // One launch: the owner workgroups (params p) followed by pd.nblocks
 // workgroups computing grad_loc / grad_attn (params pd, runtime shape).
 hipError_t launch_owner(int dtype, bool fused, const Params& p, const Params& pd,
