@@ -298,7 +298,7 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
   // Store a finished row sum: plain in the first round, added to the row's
   // earlier value in later rounds (this workgroup is the row's only writer).
   auto put = [&](int r, const float (&acc)[kVec], bool written) {
-    const uint32_t off = rbase + (uint32_t)r * rstride;
+    const uint32_t off = rbase + __umul24((uint32_t)r, rstride);  // both < 2^24
     float v[kVec];
 #pragma unroll
     for (int k = 0; k < kVec; ++k) v[k] = acc[k];
@@ -482,19 +482,15 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
 #pragma unroll
       for (int k = 0; k < kVec; ++k) first[k] = acc[k] = 0.f;
       if (e_lo < e_hi) {
-        int cur = __float_as_int(u.csr[e_lo].y) >> kOwnQBits;
-        auto flush = [&]() {
-          const int rs0 = s_off[cur] - base, re0 = s_off[cur + 1] - base;
-          if (rs0 < e_lo) {
-#pragma unroll
-            for (int k = 0; k < kVec; ++k) first[k] = acc[k];
-            has_first = true;
-          } else if (re0 > e_hi) {
-            tail_row = cur;  // acc stays the tail
-          } else {
-            put(cur, acc, written);
-          }
-        };
+        // The slice's first row may have begun in an earlier slice (then
+        // its sum here is a piece, kept in `first`); every other row that
+        // ends inside the slice is complete.  Only the last row can run on
+        // past the slice.  So the row boundaries inside the loop need no
+        // offset lookups.
+        const int row0 = __float_as_int(u.csr[e_lo].y) >> kOwnQBits;
+        const bool first_part = s_off[row0] - base < e_lo;
+        int cur = row0;
+        const uint32_t gb = (uint32_t)chg;
         for (int e0 = e_lo; e0 < e_hi; e0 += 4) {
           float2 en[4];
 #pragma unroll
@@ -502,16 +498,23 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             if (e0 + k < e_hi) {
-              const int bits = __float_as_int(en[k].y);
-              const int r = bits >> kOwnQBits;
-              if (r != cur) {
-                flush();
+              const uint32_t bits = (uint32_t)__float_as_int(en[k].y);
+              const int r = (int)(bits >> kOwnQBits);
+              if (r != cur) {  // row cur ends here
+                if (cur == row0 && first_part) {
+#pragma unroll
+                  for (int v = 0; v < kVec; ++v) first[v] = acc[v];
+                  has_first = true;
+                } else {
+                  put(cur, acc, written);
+                }
 #pragma unroll
                 for (int v = 0; v < kVec; ++v) acc[v] = 0.f;
                 cur = r;
               }
+              // g offset: query < 2^11, row bytes <= 256 (24-bit multiply)
               const uint4 raw = *reinterpret_cast<const uint4*>(
-                  s_g + (bits & ((1 << kOwnQBits) - 1)) * rowb + chg);
+                  s_g + (__umul24(bits & ((1u << kOwnQBits) - 1), (uint32_t)rowb) + gb));
               const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
               float gv[kVec];
               C::unpack(w4, gv);
@@ -520,7 +523,15 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
             }
           }
         }
-        flush();
+        if (cur == row0 && first_part) {  // a piece (the slice lies inside one row)
+#pragma unroll
+          for (int v = 0; v < kVec; ++v) first[v] = acc[v];
+          has_first = true;
+        } else if (s_off[cur + 1] - base > e_hi) {
+          tail_row = cur;  // acc stays the tail
+        } else {
+          put(cur, acc, written);
+        }
       }
       __syncthreads();  // every entry read: the pieces may overwrite the CSR
       if (has_first) {
