@@ -47,11 +47,11 @@ namespace msda {
 
 namespace {
 
-constexpr int kOwnRows = 4 * kBlock;       // pixels per band, at most (4 per lane in the scan)
+constexpr int kOwnRows = 8 * kBlock;       // pixels per band, at most (8 per lane in the scan)
 constexpr int kOwnCap = 2048;              // CSR entries per sub-band; path needs Q * K <= it
 constexpr int kOwnBandFill = kOwnCap * 4 / 5;  // corner entries per band, at most (level split)
 constexpr int kOwnEntriesPerNs = 100;      // least entries per band per sample slot (level split)
-constexpr int kOwnGBytes = 5 * 16 * kBlock;  // staged grad_out rows (Q * D * elem), at most
+constexpr int kOwnGBytes = 19456;          // staged grad_out rows (Q * D * elem), at most
 
 // Band [lo, hi) of group gi of a (b, m); false for groups past the last band.
 __device__ bool own_band(const Params& p, const LevelTable& lt, int gi, int& lo, int& hi) {
@@ -179,12 +179,13 @@ template <int kVec>
 struct OwnLds {
   LevelTable lt;
   uint16_t s_off[kOwnRows + 8];  // CSR offsets (exclusive prefix sum of the counts)
-  // Entries per row counted per wave (count pass), then each wave's
-  // exclusive prefix over the waves; then the CSR entries (A * w_c, query |
-  // local row << kOwnQBits), rows contiguous; then, after the entries are
-  // read, each team's piece of the row it continues from the slice before.
+  // Entries per row counted per wave (count pass; 16-bit counters, rows 2k
+  // and 2k + 1 in word k), then each wave's exclusive prefix over the
+  // waves; then the CSR entries (A * w_c, query | local row << kOwnQBits),
+  // rows contiguous; then, after the entries are read, each team's piece of
+  // the row it continues from the slice before.
   union {
-    int cnt[kBlock / kWave][kOwnRows];
+    uint32_t cnt[kBlock / kWave][kOwnRows / 2];
     float2 csr[kOwnCap];
     float piece[kBlock * kVec];
   } u;
@@ -194,7 +195,7 @@ struct OwnLds {
 
 // T: storage dtype; NS: samples per lane and level (NS * kBlock >= Q * K).
 // p.g_rt lanes (a power of two, g_real of them live) cover a value row in
-// 16-byte chunks.  ~39 KB of LDS and <= 128 VGPRs: four workgroups per CU.
+// 16-byte chunks.  ~40.7 KB of LDS and <= 128 VGPRs: four workgroups per CU.
 //
 // p.nblocks workgroups own bands of grad_value; pd.nblocks more compute
 // grad_loc / grad_attn (the direct backward body without its scatter, launch
@@ -207,9 +208,9 @@ template <class T, int NS, bool FUSED, int DG>
 __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
   using C = Chunk<T, 16>;
   constexpr int kVec = C::kVec;
-  constexpr int kGIt = kOwnGBytes / 16 / kBlock;  // staged 16-byte chunks per lane
-  static_assert(kOwnRows == 4 * kBlock, "four rows per lane in the scan");
-  static_assert(kOwnGBytes % (16 * kBlock) == 0, "whole staging rounds");
+  constexpr int kGIt = (kOwnGBytes / 16 + kBlock - 1) / kBlock;  // staged 16-byte chunks per lane
+  static_assert(kOwnRows == 8 * kBlock, "eight rows per lane in the scan");
+  static_assert(kOwnGBytes % 16 == 0, "whole chunks");
   static_assert(4 * NS * kBlock < 65536, "16-bit CSR offsets");
 
   __shared__ union {
@@ -234,7 +235,7 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
   int* const s_wsum = smem.own.s_wsum;
   uint8_t* const s_g = smem.own.s_g;
 
-  const int tid = threadIdx.x;
+  int tid = threadIdx.x;
   // Grid: bid = 8 k + x runs on XCD x (round-robin dispatch).  Band group
   // bg = (k / M) * 8 + x and head m = k % M: the heads of a band share an
   // XCD (whole 128-byte lines of grad_value meet in its L2), XCDs get
@@ -317,6 +318,9 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
   for (int l = 0; l < p.L; ++l) {
     const int H = lt.h[l], W = lt.w[l], st = lt.start[l];
     if (H <= 0 || W <= 0) continue;
+    // Addresses derived from tid are recomputed in each level round rather
+    // than kept in registers across rounds (most calls have one round).
+    asm volatile("" : "+v"(tid));
     if ((int64_t)st >= hi || (int64_t)st + (int64_t)H * W <= lo) continue;
     const float fw = (float)W, fh = (float)H;
 
@@ -334,7 +338,7 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
     }
 #pragma unroll
     for (int w = 0; w < kBlock / kWave; ++w)
-      for (int r = tid; r < nrows; r += kBlock) u.cnt[w][r] = 0;
+      for (int r = tid; r < (nrows + 1) / 2; r += kBlock) u.cnt[w][r] = 0;
     __syncthreads();  // counts zeroed (and, in later rounds, the last pieces read)
 
     // 1. Entries per row.  Each wave counts into its own counters, so the
@@ -356,8 +360,12 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         rk[c] = 0;
-        if (bi & (1u << c))
-          rk[c] = atomicAdd(&u.cnt[wave][pix[i] + (c & 1) + (c >> 1) * W - lo], 1);
+        if (bi & (1u << c)) {
+          // A wave adds at most 64 * NS < 2^16 to a row: no carry between halves.
+          const int r = pix[i] + (c & 1) + (c >> 1) * W - lo;
+          const uint32_t sh = (uint32_t)(r & 1) * 16u;
+          rk[c] = (atomicAdd(&u.cnt[wave][r >> 1], 1u << sh) >> sh) & 0xffffu;
+        }
       }
       rank[2 * i] = rk[0] | rk[1] << 16;
       rank[2 * i + 1] = rk[2] | rk[3] << 16;
@@ -367,28 +375,32 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
     // 2. CSR offsets of the rows' totals; each wave's counter becomes the
     // sum over the waves before it.
     {
-      int c4[4], sum = 0;
+      // Row totals < 2^16 (a row takes at most one corner per sample), so
+      // two share a word here too.
+      uint32_t c2[4];
+      int sum = 0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int r = tid * 4 + k;
-        c4[k] = 0;
-        if (r < nrows) {
+        const int wd = tid * 4 + k;  // rows 2 wd, 2 wd + 1
+        uint32_t c = 0;
+        if (2 * wd < nrows) {
 #pragma unroll
           for (int w = 0; w < kBlock / kWave; ++w) {
-            const int n = u.cnt[w][r];
-            u.cnt[w][r] = c4[k];
-            c4[k] += n;
+            const uint32_t n = u.cnt[w][wd];
+            u.cnt[w][wd] = c;
+            c += n;  // both halves at once: no half exceeds 2^16
           }
         }
-        sum += c4[k];
+        c2[k] = c;
+        sum += (int)((c & 0xffffu) + (c >> 16));
       }
       int tot;
       int ex = own_scan(sum, s_wsum, &tot);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int r = tid * 4 + k;
+      for (int k = 0; k < 8; ++k) {
+        const int r = tid * 8 + k;
         if (r < nrows) s_off[r] = (uint16_t)ex;
-        ex += c4[k];
+        ex += (int)((c2[k >> 1] >> ((k & 1) * 16)) & 0xffffu);
       }
       if (tid == 0) s_off[nrows] = (uint16_t)tot;
     }
@@ -402,7 +414,8 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const bool in = (bits >> (4 * i + c)) & 1u;
-        before[c] = u.cnt[wave][in ? pix[i] + (c & 1) + (c >> 1) * W - lo : 0];
+        const int r = in ? pix[i] + (c & 1) + (c >> 1) * W - lo : 0;
+        before[c] = (int)((u.cnt[wave][r >> 1] >> ((r & 1) * 16)) & 0xffffu);
         if (!in) before[c] = 0;
       }
       rank[2 * i] += (uint32_t)before[0] | (uint32_t)before[1] << 16;
@@ -623,7 +636,6 @@ bool owner_plan(int64_t B, int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L
   if (rowb <= 0 || rowb % 16 != 0 || rowb / 16 > 16) return false;
   if (Q * K <= 0 || Q * K > kOwnCap || Q * rowb > kOwnGBytes) return false;
   if (S <= 0 || L <= 0) return false;
-  const int64_t rows = own_env("MSDA_OWN_ROWS", kOwnRows, 64, kOwnRows);
   // Bands per level: at least ceil(H * W / rows), and at least `split`,
   // which spreads a level's corner entries (up to 4 Q K) over bands.  More
   // bands run in parallel but each scans all Q K samples of its level, so
@@ -634,20 +646,35 @@ bool owner_plan(int64_t B, int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L
   // on MI355X (decoder pyramid, B=1/2/4/8, Q*K=400/1200; tiny): within 5%
   // of the best fixed split in every case, 1.2-1.6x faster than one split
   // for all.  The host does not see H and W (they live on the device), so
-  // bands are estimated from S and L.
+  // bands are estimated from S and L.  Rows per band: kOwnRows where the
+  // grid still fills ~80% of a round with them (fewer bands scan the fine
+  // level's samples: decoder B=4 23.9 against 24.6 us, B=8 37.5 against
+  // 42.5), else half that (small grids: a band's own time is the kernel's).
   const int64_t ent = 4 * Q * K;
-  int64_t split;
-  if (getenv("MSDA_OWN_ENTRIES")) {
-    const int64_t target = own_env("MSDA_OWN_ENTRIES", kOwnBandFill, 64, 1 << 20);
-    split = (ent + target - 1) / target;
-  } else {
+  const int64_t want = own_slots() * 4 / 5;
+  const bool env_split = getenv("MSDA_OWN_ENTRIES") != nullptr;
+  auto plan_split = [&](int64_t rows, bool* full) {
+    const int64_t fine = (S + rows - 1) / rows;
+    auto wgs = [&](int64_t s) { return B * p->M * (std::max(fine, s) + (L - 1) * s); };
+    if (env_split) {
+      const int64_t target = own_env("MSDA_OWN_ENTRIES", kOwnBandFill, 64, 1 << 20);
+      *full = true;
+      return (ent + target - 1) / target;
+    }
     const int64_t ns = (Q * K + kBlock - 1) / kBlock;
     const int64_t lo = (ent + kOwnBandFill - 1) / kOwnBandFill;
     const int64_t hi = std::max(lo, ent / (kOwnEntriesPerNs * ns));
-    const int64_t want = own_slots() * 4 / 5;
-    const int64_t fine = (S + rows - 1) / rows;
-    split = lo;
-    while (split < hi && B * p->M * (std::max(fine, split) + (L - 1) * split) < want) ++split;
+    int64_t s = lo;
+    while (s < hi && wgs(s) < want) ++s;
+    *full = wgs(s) >= want;
+    return s;
+  };
+  int64_t rows = own_env("MSDA_OWN_ROWS", kOwnRows, 64, kOwnRows);
+  bool full = true;
+  int64_t split = plan_split(rows, &full);
+  if (!full && !getenv("MSDA_OWN_ROWS")) {
+    rows = kOwnRows / 2;
+    split = plan_split(rows, &full);
   }
   const int64_t groups = (S + rows - 1) / rows + L * (1 + split);
   if (groups * (int64_t)p->M * 64 >= (1ll << 31)) return false;
