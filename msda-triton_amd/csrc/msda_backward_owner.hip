@@ -53,35 +53,53 @@ constexpr int kOwnBandFill = kOwnCap * 4 / 5;  // corner entries per band, at mo
 constexpr int kOwnEntriesPerNs = 100;      // least entries per band per sample slot (level split)
 constexpr int kOwnGBytes = 19456;          // staged grad_out rows (Q * D * elem), at most
 
-// Band [lo, hi) of group gi of a (b, m); false for groups past the last band.
-__device__ bool own_band(const Params& p, const LevelTable& lt, int gi, int& lo, int& hi) {
-  bool standard = true;
+// Level l's (H, W, start) read from the caller's int64 tensors.  The index
+// is uniform and nothing has been stored yet where this is called, so these
+// are scalar loads: a workgroup learns its band before any vector load, and
+// groups past the last band leave at once, freeing their slot.
+struct OwnLevel {
+  int h, w, start;
+};
+__device__ __forceinline__ OwnLevel own_level(const Params& p, int l) {
+  return {(int)p.shapes[2 * l], (int)p.shapes[2 * l + 1], (int)p.starts[l]};
+}
+
+// Band [lo, hi) of group gi of a (b, m).  Returns 1 for a band of the
+// cumulative level table (it lies in level lv, whose (H, W, start) is `lev`),
+// 2 for a band of another table (every level that meets it is processed), 0
+// for groups past the last band.  Same answer in every lane.
+__device__ int own_band(const Params& p, int gi, int& lo, int& hi, int& lv, OwnLevel& lev) {
+  // One pass: the table check and, assuming the table is the cumulative
+  // one, the band's level (unrolled so that the scalar loads overlap).
+  bool standard = true, found = false;
   int64_t acc = 0;
+  int g = gi;
+#pragma unroll 4
   for (int l = 0; l < p.L; ++l) {
-    if (lt.h[l] < 0 || lt.w[l] < 0 || (int64_t)lt.start[l] != acc) standard = false;
-    acc += (int64_t)lt.h[l] * lt.w[l];
-  }
-  if (acc != (int64_t)p.S) standard = false;
-  if (standard) {
-    for (int l = 0; l < p.L; ++l) {
-      const int hw = lt.h[l] * lt.w[l];
-      if (hw == 0) continue;
+    const OwnLevel v = own_level(p, l);
+    if (v.h < 0 || v.w < 0 || (int64_t)v.start != acc) standard = false;
+    acc += (int64_t)v.h * v.w;
+    const int hw = v.h * v.w;
+    if (!found && hw > 0) {
       int n = (hw + p.own_rows - 1) / p.own_rows;
       if (n < p.own_split) n = p.own_split;
       if (n > hw) n = hw;
-      if (gi < n) {
+      if (g < n) {
         const int size = (hw + n - 1) / n;
-        lo = lt.start[l] + gi * size;
-        hi = min(lo + size, lt.start[l] + hw);
-        return lo < hi;
+        lo = v.start + g * size;
+        hi = min(lo + size, v.start + hw);
+        lv = l;
+        lev = v;
+        found = true;
       }
-      gi -= n;
+      g -= n;
     }
-    return false;
   }
+  if (acc != (int64_t)p.S) standard = false;
+  if (standard) return found && lo < hi ? 1 : 0;
   lo = gi * p.own_rows;
   hi = min(lo + p.own_rows, p.S);
-  return lo < hi;
+  return lo < hi ? 2 : 0;
 }
 
 // Exclusive prefix sum over the workgroup; `tot` receives the total.
@@ -249,10 +267,15 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
   const int gi = bg / nb;
   if (gi >= p.own_groups) return;  // grid padding
 
+  int lo, hi, lv0 = 0;
+  OwnLevel lev0 = {0, 0, 0};
+  const int kind = own_band(p, gi, lo, hi, lv0, lev0);
+  if (kind == 0) return;  // past the last band
+
   const int rowb = p.D * T::kBytes;  // g_real * 16 (path condition)
   const int nsmp = p.Q * p.K;
-  // Stage grad_out[b, :, m, :]: loads issued before the level table's round
-  // trip, written to LDS after it (chunk k of the stage is its byte k * 16).
+  // Stage grad_out[b, :, m, :] (chunk k of the stage is its byte k * 16);
+  // other level tables also take an LDS copy of the table meanwhile.
   const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.grad_out, p.gout_bytes);
   const uint32_t gq0 = ((uint32_t)b * (uint32_t)p.Q * (uint32_t)p.M + (uint32_t)m) * (uint32_t)rowb;
   const uint32_t gqs = (uint32_t)p.M * (uint32_t)rowb;  // grad_out stride between queries
@@ -266,15 +289,14 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
                                      : 0x80000000u;
     graw[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0);
   }
-  load_levels(p, lt);
+  if (kind == 2) load_levels(p, lt);
 #pragma unroll
   for (int k = 0; k < kGIt; ++k) {
     const int kk = tid + k * kBlock;
     if (kk < nchunk) *reinterpret_cast<i32x4*>(s_g + kk * 16) = graw[k];
   }
   __syncthreads();
-  int lo, hi;
-  if (!own_band(p, lt, gi, lo, hi)) return;  // same answer in every lane
+  const int l_begin = kind == 1 ? lv0 : 0, l_end = kind == 1 ? lv0 + 1 : p.L;
 
   const int G = p.g_rt, lg = p.own_lg;  // lanes per row and its log2
   const int kTeams = kBlock >> lg;
@@ -315,8 +337,10 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
   };
 
   bool written = false;
-  for (int l = 0; l < p.L; ++l) {
-    const int H = lt.h[l], W = lt.w[l], st = lt.start[l];
+  for (int l = l_begin; l < l_end; ++l) {
+    const int H = kind == 1 ? lev0.h : lt.h[l];
+    const int W = kind == 1 ? lev0.w : lt.w[l];
+    const int st = kind == 1 ? lev0.start : lt.start[l];
     if (H <= 0 || W <= 0) continue;
     // Addresses derived from tid are recomputed in each level round rather
     // than kept in registers across rounds (most calls have one round).
