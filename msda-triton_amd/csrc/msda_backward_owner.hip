@@ -274,28 +274,34 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
 
   const int rowb = p.D * T::kBytes;  // g_real * 16 (path condition)
   const int nsmp = p.Q * p.K;
-  // Stage grad_out[b, :, m, :] (chunk k of the stage is its byte k * 16);
-  // other level tables also take an LDS copy of the table meanwhile.
+  // Stage grad_out[b, :, m, :] (chunk k of the stage is its byte k * 16)
+  // with loads that write LDS directly (lane i of a wave's load lands at
+  // the wave's base + 16 i): no registers held, and they complete while the
+  // parameter loads are in flight -- the first barrier after those waits
+  // for both.  Waves whose chunks all lie past the last one issue nothing;
+  // the stage's size is a multiple of a wave's 64 chunks, so a wave that
+  // issues stays inside it.
+  static_assert(kOwnGBytes % (16 * kWave) == 0, "whole waves of chunks");
   const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.grad_out, p.gout_bytes);
   const uint32_t gq0 = ((uint32_t)b * (uint32_t)p.Q * (uint32_t)p.M + (uint32_t)m) * (uint32_t)rowb;
   const uint32_t gqs = (uint32_t)p.M * (uint32_t)rowb;  // grad_out stride between queries
   const int nchunk = p.Q * p.g_real;
-  i32x4 graw[kGIt];
 #pragma unroll
   for (int k = 0; k < kGIt; ++k) {
     const int kk = tid + k * kBlock;
-    const int q = (int)fdiv((uint32_t)kk, p.div_g);
-    const uint32_t off = kk < nchunk ? gq0 + (uint32_t)q * gqs + (uint32_t)(kk - q * p.g_real) * 16u
-                                     : 0x80000000u;
-    graw[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0);
+    const int k0 = kk & ~(kWave - 1);  // the wave's first chunk (uniform)
+    if (k0 < nchunk) {
+      const int q = (int)fdiv((uint32_t)kk, p.div_g);
+      const uint32_t off = kk < nchunk ? gq0 + (uint32_t)q * gqs + (uint32_t)(kk - q * p.g_real) * 16u
+                                       : 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rg, (__attribute__((address_space(3))) void*)(s_g + k0 * 16), 16, off, 0, 0, 0);
+    }
   }
-  if (kind == 2) load_levels(p, lt);
-#pragma unroll
-  for (int k = 0; k < kGIt; ++k) {
-    const int kk = tid + k * kBlock;
-    if (kk < nchunk) *reinterpret_cast<i32x4*>(s_g + kk * 16) = graw[k];
+  if (kind == 2) {  // other level tables: an LDS copy
+    load_levels(p, lt);
+    __syncthreads();
   }
-  __syncthreads();
   const int l_begin = kind == 1 ? lv0 : 0, l_end = kind == 1 ? lv0 + 1 : p.L;
 
   const int G = p.g_rt, lg = p.own_lg;  // lanes per row and its log2
