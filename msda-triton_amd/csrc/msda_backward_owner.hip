@@ -507,10 +507,17 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
       __syncthreads();
 
       // Rows without entries: zeros in the first round, untouched later.
+      // Four rows per team and step, their offsets read together.
       if (!written) {
         const float zero[kVec] = {};
-        for (int r = r0 + team; r < r1; r += kTeams)
-          if (s_off[r + 1] == s_off[r]) put(r, zero, false);
+        for (int rb = r0 + team * 4; rb < r1; rb += kTeams * 4) {
+          int o[5];
+#pragma unroll
+          for (int k = 0; k < 5; ++k) o[k] = s_off[min(rb + k, r1)];
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            if (rb + k < r1 && o[k + 1] == o[k]) put(rb + k, zero, false);
+        }
       }
 
       // Entries: team t sums slice [t * cs, (t + 1) * cs) of the CSR.  A row
