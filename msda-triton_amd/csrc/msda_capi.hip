@@ -313,10 +313,11 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
         po.g_real = own.g_real;
         po.g_rt = own.g_rt;
         po.own_lg = own.own_lg;
+        po.own_est = own.own_est;
         po.div_g = make_fastdiv((uint32_t)own.g_real);
-        {  // sweeps: MSDA_OWN_MIX=1 gradient workgroups first, -1 two launches
+        {  // sweeps: MSDA_OWN_MIX=0 gradient workgroups last, 1 first, -1 two launches
           const char* mx = getenv("MSDA_OWN_MIX");
-          po.own_mix = mx ? atoi(mx) : 0;
+          po.own_mix = mx ? atoi(mx) : 2;
         }
         if (f) po.ref_bytes = (uint32_t)(nb * ref_per_b * e);
         finish_params(sh, kBwdRecords, &p);

@@ -371,7 +371,9 @@ struct Params {
   int32_t own_lg;      //   log2 of the lanes per row (g_rt)
   FastDiv div_g;       //   division by g_real (live lanes per row)
   uint32_t ref_bytes;  //   fused: num_records of the reference points
-  int32_t own_mix;     //   order of band and gradient workgroups (1: gradient workgroups first, 0: last)
+  int32_t own_mix;     //   order of band and gradient workgroups (0 last, 1 first, 2 after own_est)
+  int32_t own_est;     //   bands per (b, m), estimated (host)
+  int32_t own_cut;     //   band chunks (of 8 workgroups) dispatched before the gradient chunks
   FastDiv div_qm, div_m, div_k, div_d;
 };
 

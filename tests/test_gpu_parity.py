@@ -204,6 +204,7 @@ OVERRIDES = [
     dict(MSDA_BWD_OWNER="0", MSDA_BWD_PRIV="0"),     # direct backward, 16 lanes/row
     dict(MSDA_BWD_OWNER="0", MSDA_BWD_PRIV="0", MSDA_BWD_CB="16", MSDA_BWD_TS="4"),
     dict(MSDA_BWD_OWNER="0", MSDA_BWD_PRIV="0", MSDA_BWD_CB="8", MSDA_BWD_TS="16"),
+    dict(MSDA_OWN_MIX="0"),                          # owner path, gradient workgroups last
     dict(MSDA_OWN_MIX="1"),                          # owner path, gradient workgroups first
     dict(MSDA_OWN_MIX="-1"),                         # owner path, gradient kernel launched apart
     dict(MSDA_FWD_TS="1", MSDA_FWD_CB="8"),          # owner path, other dot-kernel shapes
