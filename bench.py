@@ -507,10 +507,10 @@ def main() -> int:
     def capture(fn, reps):
         return _capture(fn, reps, dev)
 
-    # Steps are replayed from HIP graphs of up to 10 back-to-back steps (the
-    # host's per-replay launch cost, ~5 us, is then paid once per 10 steps);
+    # Steps are replayed from HIP graphs of up to 50 back-to-back steps (the
+    # host's per-replay launch cost, ~5 us, is then paid once per 50 steps);
     # a second graph takes the remainder, so exactly K steps run.
-    per_graph = max(1, min(10, args.steps))
+    per_graph = max(1, min(50, args.steps))
     step_graph = capture(step, per_graph)
     rest = args.steps % per_graph
     rest_graph = capture(step, rest) if rest else None
@@ -603,7 +603,7 @@ def main() -> int:
             "B": B, "Q": Q, "M": M, "D": D, "L": L, "K": K, "S": S,
             "spatial_shapes": c["shapes"],
             "grad_value_accum": "fp32" if accum is not None else dtype_name,
-            "timing": "HIP-graph replay of C-ABI calls (10 steps per graph); inputs "
+            "timing": "HIP-graph replay of C-ABI calls (50 steps per graph); inputs "
                       "resident in HBM",
         },
         "fwd_us": round(fwd_us, 3),
