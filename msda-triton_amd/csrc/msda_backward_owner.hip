@@ -542,11 +542,20 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
         const int row0 = __float_as_int(u.csr[e_lo].y) >> kOwnQBits;
         const bool first_part = s_off[row0] - base < e_lo;
         int cur = row0;
+        // g offsets: query < 2^11, row bytes <= 256 (24-bit multiply)
         const uint32_t gb = (uint32_t)chg;
         for (int e0 = e_lo; e0 < e_hi; e0 += 4) {
           float2 en[4];
 #pragma unroll
           for (int k = 0; k < 4; ++k) en[k] = u.csr[min(e0 + k, e_hi - 1)];
+          // The four entries' grad_out chunks, read together (their LDS
+          // latencies overlap instead of one wait per entry).
+          uint4 graw4[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            graw4[k] = *reinterpret_cast<const uint4*>(
+                s_g + (__umul24((uint32_t)__float_as_int(en[k].y) & ((1u << kOwnQBits) - 1),
+                                (uint32_t)rowb) + gb));
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             if (e0 + k < e_hi) {
@@ -564,10 +573,7 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
                 for (int v = 0; v < kVec; ++v) acc[v] = 0.f;
                 cur = r;
               }
-              // g offset: query < 2^11, row bytes <= 256 (24-bit multiply)
-              const uint4 raw = *reinterpret_cast<const uint4*>(
-                  s_g + (__umul24(bits & ((1u << kOwnQBits) - 1), (uint32_t)rowb) + gb));
-              const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+              const uint32_t w4[4] = {graw4[k].x, graw4[k].y, graw4[k].z, graw4[k].w};
               float gv[kVec];
               C::unpack(w4, gv);
 #pragma unroll
