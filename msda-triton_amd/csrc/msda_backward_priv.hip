@@ -451,8 +451,7 @@ __global__ __launch_bounds__(kBlock) void bwd_priv_kernel(Params p) {
       const uint64_t pi = pair * (uint32_t)p.LK + (uint32_t)(l * K + k);
       const float4 r = s_res[tid];
       store1<T>(p.grad_attn, pi, r.x);
-      store1<T>(p.grad_loc, 2 * pi, r.y);
-      store1<T>(p.grad_loc, 2 * pi + 1, r.z);
+      store_xy<T>(p.grad_loc, pi, r.y, r.z);
     }
   }
 }

@@ -176,8 +176,7 @@ __device__ __forceinline__ void bwd_body(const Params& p, int blk, BwdLds& sm) {
         const uint64_t pi = (uint64_t)pr * (uint32_t)p.LK + (uint32_t)s;
         const float4 r = s_res[j];
         store1<T>(p.grad_attn, pi, r.x);
-        store1<T>(p.grad_loc, 2 * pi, r.y);
-        store1<T>(p.grad_loc, 2 * pi + 1, r.z);
+        store_xy<T>(p.grad_loc, pi, r.y, r.z);
       }
     }
     if (pass + 1 < p.npass) __syncthreads();

@@ -149,6 +149,25 @@ __device__ __forceinline__ void store1<BF16>(void* base, uint64_t i, float v) {
   static_cast<__bf16*>(base)[i] = (__bf16)v;
 }
 
+// Elements 2i and 2i + 1 (an (x, y) pair): one store when the base allows
+// it (16-bit types: 4-byte aligned; fp32: 8-byte aligned), else two.
+template <class T>
+__device__ __forceinline__ void store_xy(void* base, uint64_t i, float x, float y) {
+  if constexpr (T::kBytes == 4) {
+    if ((reinterpret_cast<uintptr_t>(base) & 7) == 0) {
+      static_cast<float2*>(base)[i] = make_float2(x, y);
+      return;
+    }
+  } else {
+    if ((reinterpret_cast<uintptr_t>(base) & 3) == 0) {
+      static_cast<uint32_t*>(base)[i] = pack2<T>(x, y);
+      return;
+    }
+  }
+  store1<T>(base, 2 * i, x);
+  store1<T>(base, 2 * i + 1, y);
+}
+
 template <class T>
 __device__ __forceinline__ float load1(const void* base, uint64_t i) {
   if constexpr (T::kBytes == 4) {
