@@ -95,7 +95,7 @@ int msda_forward(const void* value, const int64_t* spatial_shapes,
  * The library picks one of three ways to form grad_value
  * (msda_backward_plan reports which): for few samples per (batch, head,
  * level) -- Q*K <= 2048, a head row of a multiple of 16 bytes up to 256,
- * Q*D*elem <= 19456, 16-byte aligned grad_output and grad_value -- workgroups
+ * Q*D*elem <= 40960, 16-byte aligned grad_output and grad_value -- workgroups
  * that own bands of value rows sum each element's contributions in fp32 and
  * store it once (no atomics, no zero-fill, grad_value_accum unused);
  * otherwise grad_value is zero-filled on `stream` and accumulated with

@@ -52,6 +52,9 @@ constexpr int kOwnCap = 2048;              // CSR entries per sub-band; path nee
 constexpr int kOwnBandFill = kOwnCap * 4 / 5;  // corner entries per band, at most (level split)
 constexpr int kOwnEntriesPerNs = 100;      // least entries per band per sample slot (level split)
 constexpr int kOwnGBytes = 19456;          // staged grad_out rows (Q * D * elem), at most
+// A second build of the kernel stages up to kOwnGBytesBig (fp32 decoders,
+// Q * D * elem up to 40 KB) at two workgroups per CU instead of four.
+constexpr int kOwnGBytesBig = 40960;
 
 // Level l's (H, W, start) read from the caller's int64 tensors.  The index
 // is uniform and nothing has been stored yet where this is called, so these
@@ -193,7 +196,7 @@ constexpr int kOwnQBits = 11;  // query index in a CSR entry (Q <= Q * K <= kOwn
 static_assert(kOwnCap <= (1 << kOwnQBits), "query index field");
 
 // LDS of an owner workgroup.
-template <int kVec>
+template <int kVec, int GB>
 struct OwnLds {
   LevelTable lt;
   uint16_t s_off[kOwnRows + 8];  // CSR offsets (exclusive prefix sum of the counts)
@@ -208,7 +211,7 @@ struct OwnLds {
     float piece[kBlock * kVec];
   } u;
   int s_wsum[kBlock / kWave];
-  alignas(16) uint8_t s_g[kOwnGBytes];  // grad_out rows of (b, m): Q x D * elem
+  alignas(16) uint8_t s_g[GB];  // grad_out rows of (b, m): Q x D * elem
 };
 
 // T: storage dtype; NS: samples per lane and level (NS * kBlock >= Q * K).
@@ -222,17 +225,18 @@ struct OwnLds {
 // of running as two launches (decoder preset: 28 us against 32 us).
 // DG > 0: the gradient workgroups' shape is 16-byte chunks, DG lanes per
 // row, 4 slots (compiled); 0: pd's runtime shape (16-byte chunks).
-template <class T, int NS, bool FUSED, int DG>
+// GB: bytes of staged grad_out (kOwnGBytes or kOwnGBytesBig).
+template <class T, int NS, bool FUSED, int DG, int GB>
 __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
   using C = Chunk<T, 16>;
   constexpr int kVec = C::kVec;
-  constexpr int kGIt = (kOwnGBytes / 16 + kBlock - 1) / kBlock;  // staged 16-byte chunks per lane
+  constexpr int kGIt = (GB / 16 + kBlock - 1) / kBlock;  // staged 16-byte chunks per lane
   static_assert(kOwnRows == 8 * kBlock, "eight rows per lane in the scan");
-  static_assert(kOwnGBytes % 16 == 0, "whole chunks");
+  static_assert(GB % 16 == 0, "whole chunks");
   static_assert(4 * NS * kBlock < 65536, "16-bit CSR offsets");
 
   __shared__ union {
-    OwnLds<kVec> own;
+    OwnLds<kVec, GB> own;
     BwdLds grad;
   } smem;
   // Chunks of 8 consecutive workgroups (one per XCD): p.own_cut band
@@ -283,7 +287,7 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
   // for both.  Waves whose chunks all lie past the last one issue nothing;
   // the stage's size is a multiple of a wave's 64 chunks, so a wave that
   // issues stays inside it.
-  static_assert(kOwnGBytes % (16 * kWave) == 0, "whole waves of chunks");
+  static_assert(GB % (16 * kWave) == 0, "whole waves of chunks");
   const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.grad_out, p.gout_bytes);
   const uint32_t gq0 = ((uint32_t)b * (uint32_t)p.Q * (uint32_t)p.M + (uint32_t)m) * (uint32_t)rowb;
   const uint32_t gqs = (uint32_t)p.M * (uint32_t)rowb;  // grad_out stride between queries
@@ -625,10 +629,21 @@ hipError_t launch_ns(const Params& p, const Params& pd, hipStream_t st) {
   const int grid = p.nblocks + (pd.nblocks + 7) / 8 * 8;  // p.nblocks: a multiple of 8
   // Compiled gradient shape for 32-channel rows (2 * elem lanes of 16 bytes).
   constexpr int kDG = 2 * T::kBytes;
-  if (pd.g_rt == kDG && pd.ts_rt == 4) {
-    hipLaunchKernelGGL((owner_kernel<T, NS, FUSED, kDG>), dim3(grid), dim3(kBlock), 0, st, p, pd);
+  const bool dg = pd.g_rt == kDG && pd.ts_rt == 4;
+  if (p.own_big) {
+    if (dg) {
+      hipLaunchKernelGGL((owner_kernel<T, NS, FUSED, kDG, kOwnGBytesBig>), dim3(grid), dim3(kBlock),
+                         0, st, p, pd);
+    } else {
+      hipLaunchKernelGGL((owner_kernel<T, NS, FUSED, 0, kOwnGBytesBig>), dim3(grid), dim3(kBlock),
+                         0, st, p, pd);
+    }
+  } else if (dg) {
+    hipLaunchKernelGGL((owner_kernel<T, NS, FUSED, kDG, kOwnGBytes>), dim3(grid), dim3(kBlock), 0,
+                       st, p, pd);
   } else {
-    hipLaunchKernelGGL((owner_kernel<T, NS, FUSED, 0>), dim3(grid), dim3(kBlock), 0, st, p, pd);
+    hipLaunchKernelGGL((owner_kernel<T, NS, FUSED, 0, kOwnGBytes>), dim3(grid), dim3(kBlock), 0,
+                       st, p, pd);
   }
   return hipGetLastError();
 }
@@ -660,8 +675,8 @@ static int64_t own_env(const char* name, int64_t dflt, int64_t lo, int64_t hi) {
   return x < lo ? lo : x > hi ? hi : x;
 }
 
-// Workgroup slots of the current device for this kernel: four per CU.
-static int64_t own_slots() {
+// Workgroup slots of the current device for this kernel: `per_cu` per CU.
+static int64_t own_slots(int per_cu) {
   static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
@@ -672,14 +687,15 @@ static int64_t own_slots() {
       n = 256;
     cus[dev].store(n, std::memory_order_relaxed);
   }
-  return 4 * (int64_t)n;
+  return per_cu * (int64_t)n;
 }
 
 bool owner_plan(int64_t B, int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L,
                 int elem_bytes, Params* p) {
   const int64_t rowb = D * elem_bytes;
   if (rowb <= 0 || rowb % 16 != 0 || rowb / 16 > 16) return false;
-  if (Q * K <= 0 || Q * K > kOwnCap || Q * rowb > kOwnGBytes) return false;
+  if (Q * K <= 0 || Q * K > kOwnCap || Q * rowb > kOwnGBytesBig) return false;
+  const bool big = Q * rowb > kOwnGBytes;  // the 40 KB staging build, 2 per CU
   if (S <= 0 || L <= 0) return false;
   // Bands per level: at least ceil(H * W / rows), and at least `split`,
   // which spreads a level's corner entries (up to 4 Q K) over bands.  More
@@ -696,7 +712,7 @@ bool owner_plan(int64_t B, int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L
   // level's samples: decoder B=4 23.9 against 24.6 us, B=8 37.5 against
   // 42.5), else half that (small grids: a band's own time is the kernel's).
   const int64_t ent = 4 * Q * K;
-  const int64_t want = own_slots() * 4 / 5;
+  const int64_t want = own_slots(big ? 2 : 4) * 4 / 5;
   const bool env_split = getenv("MSDA_OWN_ENTRIES") != nullptr;
   auto plan_split = [&](int64_t rows, bool* full) {
     const int64_t fine = (S + rows - 1) / rows;
@@ -724,6 +740,7 @@ bool owner_plan(int64_t B, int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L
   const int64_t groups = (S + rows - 1) / rows + L * (1 + split);
   if (groups * (int64_t)p->M * 64 >= (1ll << 31)) return false;
   p->own_rows = (int32_t)rows;
+  p->own_big = big ? 1 : 0;
   p->own_split = (int32_t)split;
   {
     const int64_t fine = (S + rows - 1) / rows;

@@ -314,6 +314,7 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
         po.g_rt = own.g_rt;
         po.own_lg = own.own_lg;
         po.own_est = own.own_est;
+        po.own_big = own.own_big;
         po.div_g = make_fastdiv((uint32_t)own.g_real);
         {  // sweeps: MSDA_OWN_MIX=0 gradient workgroups last, 1 first, -1 two launches
           const char* mx = getenv("MSDA_OWN_MIX");

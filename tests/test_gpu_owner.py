@@ -61,8 +61,23 @@ def test_decoder_shapes_both_paths(dtype, owner, monkeypatch):
     value, shapes, starts, loc, attn = make_inputs(
         B=2, Q=300, M=4, D=32, shapes=[(50, 84), (25, 42), (13, 21), (7, 11)], K=4,
         dtype=dtype, device=DEVICE, loc_lo=-0.1, loc_hi=1.1)
-    expect = OWNER if owner == "1" and dtype != torch.float32 else DEDUP  # fp32: 38 KB of grad_out
+    expect = OWNER if owner == "1" else DEDUP  # fp32: 38 KB of grad_out, the 40 KB build
     assert plan(value, loc) == expect
+    g, grads = fwd_bwd(value, shapes, starts, loc, attn)
+    _, refs = run_reference_fp32(value, shapes, loc, attn, g)
+    check_grads(grads, refs, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("Q", [304, 305, 640])
+def test_grad_out_staging_builds(Q, dtype):
+    """grad_out rows of (b, m) up to 19456 bytes take the four-per-CU build,
+    up to 40960 bytes the two-per-CU one (Q * D * elem at the edges of both)."""
+    value, shapes, starts, loc, attn = make_inputs(
+        B=1, Q=Q, M=2, D=32, shapes=[(30, 40), (15, 20), (8, 10)], K=2, dtype=dtype,
+        device=DEVICE, loc_lo=-0.1, loc_hi=1.1)
+    fits = Q * 32 * value.element_size() <= 40960
+    assert plan(value, loc) == (OWNER if fits else DEDUP)
     g, grads = fwd_bwd(value, shapes, starts, loc, attn)
     _, refs = run_reference_fp32(value, shapes, loc, attn, g)
     check_grads(grads, refs, dtype)

@@ -220,13 +220,14 @@ def test_backward_plan(lib, monkeypatch):
     # encoder / Mask2Former: Q = S, far more samples per (b, m, level)
     assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 0) == dedup
     assert lib.msda_backward_plan(2, 21504, 8, 32, 21504, 3, 4, 0, 0) == dedup
-    # limits of the owner path: Q*K <= 2048, Q*D*elem <= 19456, rows of 16..256 bytes
+    # limits of the owner path: Q*K <= 2048, Q*D*elem <= 40960, rows of 16..256 bytes
     assert lib.msda_backward_plan(1, 600, 2, 32, 128, 2, 16, 1, 0) == owner  # Q*K = 2048
     assert lib.msda_backward_plan(1, 600, 2, 32, 128, 2, 17, 1, 0) == dedup
-    assert lib.msda_backward_plan(1, 600, 2, 32, 304, 2, 4, 1, 0) == owner   # 19456 B
-    assert lib.msda_backward_plan(1, 600, 2, 32, 305, 2, 4, 1, 0) == dedup
-    assert lib.msda_backward_plan(1, 600, 2, 32, 152, 2, 4, 0, 0) == owner   # 19456 B
-    assert lib.msda_backward_plan(1, 600, 2, 32, 153, 2, 4, 0, 0) == dedup
+    assert lib.msda_backward_plan(1, 600, 2, 32, 305, 2, 4, 1, 0) == owner   # 19520 B: 40 KB build
+    assert lib.msda_backward_plan(1, 600, 2, 32, 640, 2, 2, 1, 0) == owner   # 40960 B
+    assert lib.msda_backward_plan(1, 600, 2, 32, 641, 2, 2, 1, 0) == dedup
+    assert lib.msda_backward_plan(1, 600, 2, 32, 320, 2, 4, 0, 0) == owner   # 40960 B
+    assert lib.msda_backward_plan(1, 600, 2, 32, 321, 2, 4, 0, 0) == dedup
     assert lib.msda_backward_plan(1, 600, 2, 3, 100, 2, 4, 1, 0) == direct   # odd half row
     assert lib.msda_backward_plan(1, 600, 2, 128, 40, 2, 4, 1, 0) == owner   # 256-byte rows
     assert lib.msda_backward_plan(1, 600, 2, 256, 40, 2, 4, 1, 0) != owner
