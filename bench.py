@@ -406,7 +406,8 @@ def projection_times(lib, preset: str = "decoder", pad_fraction: float = 0.1) ->
     return {"preset": preset, "dtype": str(dtype).replace("torch.", ""), **res, "total": tot}
 
 
-OTHER_PRESETS = ("tiny", "encoder", "high_contention", "mask2former_fp32", "mask2former_bf16")
+OTHER_PRESETS = ("tiny", "decoder_fp16", "decoder_fp32", "encoder", "high_contention",
+                 "mask2former_fp32", "mask2former_bf16")
 
 
 def main() -> int:

@@ -122,10 +122,11 @@ __device__ __forceinline__ int own_scan(int v, int* wsum, int* tot) {
   return base + x - v;
 }
 
-// Image coordinates (x = loc_x * W - 0.5; fused: ref_x * W + offset_x - 0.5)
-// and weight A (fused: exp(logit - lse)) of one sample, rounded exactly as
-// make_sample_at rounds them.  Loads go through buffer descriptors: an
-// out-of-range offset (a lane past the last sample) reads zeros, no branch.
+// Location (fused: the image coordinate ref_x * W + offset_x - 0.5, rounded
+// as make_sample_at rounds it) and weight A (fused: exp(logit - lse)) of one
+// sample; own_cell turns them into the cell.  Loads go through buffer
+// descriptors: an out-of-range offset (a lane past the last sample) reads
+// zeros, no branch.
 struct OwnRsrc {
   __amdgpu_buffer_rsrc_t loc, attn, ref, lse;
 };
@@ -163,22 +164,31 @@ __device__ __forceinline__ void own_sample(const Params& p, const OwnRsrc& rs, u
     y = __fsub_rn(__fmaf_rn(ry, fh, v), 0.5f);
     a = expf(w - lse);
   } else {
-    x = __fsub_rn(__fmul_rn(u, fw), 0.5f);
-    y = __fsub_rn(__fmul_rn(v, fh), 0.5f);
+    x = u;  // the location itself: own_cell forms the coordinate (split_coord)
+    y = v;
     a = w;
   }
-  if (!valid) x = y = -4.f;  // a cell outside every map
+  if (!valid) x = y = FUSED ? -4.f : -1e6f;  // a cell outside every map
 }
 
-// Corner cell of (x, y): pixel index of corner 00, fractions, and the bits
-// of the corners that lie in the map and in [lo, hi) (bit c: corner c =
-// 00, 01, 10, 11 at pixel pix + (c & 1) + (c >> 1) * W).  Same floors and
-// validity as make_sample_at.
+// Corner cell of a sample: pixel index of corner 00, fractions, and the
+// bits of the corners that lie in the map and in [lo, hi) (bit c: corner c
+// = 00, 01, 10, 11 at pixel pix + (c & 1) + (c >> 1) * W).  (x, y) is the
+// image coordinate (FUSED) or the location (else); same floors, fractions
+// and validity as make_sample_at.
+template <class T, bool FUSED>
 __device__ __forceinline__ uint32_t own_cell(float x, float y, int W, int H, int st, int lo, int hi,
                                              int& pix, float& lx, float& ly) {
-  float x0f = floorf(x), y0f = floorf(y);
-  lx = x - x0f;
-  ly = y - y0f;
+  float x0f, y0f;
+  if constexpr (FUSED) {
+    x0f = floorf(x);
+    y0f = floorf(y);
+    lx = x - x0f;
+    ly = y - y0f;
+  } else {
+    coord_cell<T>(x, (float)W, x0f, lx);
+    coord_cell<T>(y, (float)H, y0f, ly);
+  }
   x0f = fminf(fmaxf(x0f, -2.f), (float)W + 1.f);
   y0f = fminf(fmaxf(y0f, -2.f), (float)H + 1.f);
   const int x0 = (int)x0f, y0 = (int)y0f;
@@ -390,7 +400,7 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
     uint32_t bits = 0;
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      const uint32_t bi = own_cell(sx[i], sy[i], W, H, st, lo, hi, pix[i], slx[i], sly[i]);
+      const uint32_t bi = own_cell<T, FUSED>(sx[i], sy[i], W, H, st, lo, hi, pix[i], slx[i], sly[i]);
       bits |= bi << (4 * i);
       uint32_t rk[4];
 #pragma unroll

@@ -499,6 +499,53 @@ struct Sample {
   uint32_t vmask;   // bit c set when corner c lies in the map
 };
 
+// Image coordinate x = a * b + c - 0.5 as a cell (x0f = floor(x)) and a
+// fraction.  The fp32 product and sum round by up to ulp(x) / 2 (W * 2^-25 px
+// for a location times a width W), which the fraction alone cannot absorb:
+// the exact rounding errors (two-product through an fma, two-sum) are added
+// to the fraction, so it is good to ~1 ulp of itself.  A half-precision
+// location times W is exact in fp32, so those inputs see no change; fp32
+// decoders (W, H not powers of two) gain ~1e-3 in grad_loc against exact
+// arithmetic.  kAdd (a sum c) is there for the fused form, which keeps its
+// single fma for now.
+template <bool kAdd>
+__device__ __forceinline__ void split_coord(float a, float b, float c, float& x0f, float& fr) {
+  const float p = __fmul_rn(a, b);
+  float err = __fmaf_rn(a, b, -p);  // a * b - p, exact
+  float s = p;
+  if constexpr (kAdd) {
+    s = __fadd_rn(p, c);
+    const float bp = __fsub_rn(s, p);
+    err = __fadd_rn(err, __fadd_rn(__fsub_rn(p, __fsub_rn(s, bp)), __fsub_rn(c, bp)));
+  }
+  const float t = __fsub_rn(s, 0.5f);
+  x0f = floorf(t);
+  float f = __fadd_rn(__fsub_rn(t, x0f), err);
+  if (f < 0.f) {
+    x0f -= 1.f;
+    f = __fadd_rn(f, 1.f);
+  } else if (f >= 1.f) {
+    x0f += 1.f;
+    f = __fsub_rn(f, 1.f);
+  }
+  fr = f;
+}
+
+// Cell and fraction of x = loc * size - 0.5 for a location in storage type
+// T: a half-precision location times an integer size is exact in fp32, so
+// one product, floor and subtraction give what split_coord gives at less
+// cost; fp32 locations take split_coord.
+template <class T>
+__device__ __forceinline__ void coord_cell(float loc, float size, float& x0f, float& fr) {
+  if constexpr (T::kBytes == 4) {
+    split_coord<false>(loc, size, 0.f, x0f, fr);
+  } else {
+    const float x = __fsub_rn(__fmul_rn(loc, size), 0.5f);
+    x0f = floorf(x);
+    fr = x - x0f;
+  }
+}
+
 //
 // make_sample_at takes the sample's level (H, W, start) explicitly (kernels
 // whose workgroup covers one level read them once instead of staging a
@@ -527,25 +574,27 @@ __device__ __forceinline__ Sample make_sample_at(const Params& p, uint32_t pair,
   const uint32_t m = pair - bq * (uint32_t)p.M;
   const uint64_t pi = (uint64_t)pair * (uint32_t)p.LK + s;
   const float fw = (float)W, fh = (float)H;
-  float x, y, a;
+  float a, x0f, y0f;
   if constexpr (FUSED) {
     const uint32_t l = fdiv(s, p.div_k);
     float rx, ry, ox, oy;
     load_xy<T>(p.ref, p.ref_levels ? (uint64_t)bq * (uint32_t)p.L + l : (uint64_t)bq, rx, ry);
     load_xy<T>(p.loc, pi, ox, oy);
-    x = __fsub_rn(__fmaf_rn(rx, fw, ox), 0.5f);
-    y = __fsub_rn(__fmaf_rn(ry, fh, oy), 0.5f);
+    // One fma, rounded once (the owner backward forms the same value).
+    const float x = __fsub_rn(__fmaf_rn(rx, fw, ox), 0.5f);
+    const float y = __fsub_rn(__fmaf_rn(ry, fh, oy), 0.5f);
+    x0f = floorf(x);
+    y0f = floorf(y);
+    r.lx = x - x0f;
+    r.ly = y - y0f;
     a = expf(load1<T>(p.attn, pi) - lse);
   } else {
     float locx, locy;
     load_xy<T>(p.loc, pi, locx, locy);
     a = load1<T>(p.attn, pi);
-    x = __fsub_rn(__fmul_rn(locx, fw), 0.5f);
-    y = __fsub_rn(__fmul_rn(locy, fh), 0.5f);
+    coord_cell<T>(locx, fw, x0f, r.lx);
+    coord_cell<T>(locy, fh, y0f, r.ly);
   }
-  float x0f = floorf(x), y0f = floorf(y);
-  r.lx = x - x0f;
-  r.ly = y - y0f;
   x0f = fminf(fmaxf(x0f, -2.f), fw + 1.f);
   y0f = fminf(fmaxf(y0f, -2.f), fh + 1.f);
   const int32_t x0 = (int32_t)x0f, y0 = (int32_t)y0f;

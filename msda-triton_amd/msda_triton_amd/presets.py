@@ -1,9 +1,9 @@
 """Benchmark presets and their seeded synthetic inputs.
 
-The five configurations are the operator's benchmark workloads (decoder and
+The configurations are the operator's benchmark workloads (decoder and
 encoder presets as in the reference's benchmarks/modal_benchmark.py:73-98,
-plus a tiny CPU-checkable case, a high-contention backward case and a
-Mask2Former-style pixel decoder).  Inputs are drawn on the CPU with a seeded
+the decoder also in fp16 and fp32, plus a tiny CPU-checkable case, a
+high-contention backward case and a Mask2Former-style pixel decoder).  Inputs are drawn on the CPU with a seeded
 ``torch.Generator`` in fp32 -- value, then locations, then attention logits
 (then grad_out, from its own seed) -- rounded to the preset dtype and only
 then moved to the device, so the GPU kernels and any CPU check see identical
@@ -29,6 +29,12 @@ PRESETS = {
     # Deformable-DETR decoder cross-attention on an 800x1333 image (headline).
     "decoder": dict(B=4, Q=300, M=8, D=32, K=4, shapes=pyramid(800, 1333),
                     dtype=torch.bfloat16, loc="uniform"),
+    # The headline decoder in the reference's other two dtypes (its README
+    # tables all three, README.md:121-124).
+    "decoder_fp16": dict(B=4, Q=300, M=8, D=32, K=4, shapes=pyramid(800, 1333),
+                         dtype=torch.float16, loc="uniform"),
+    "decoder_fp32": dict(B=4, Q=300, M=8, D=32, K=4, shapes=pyramid(800, 1333),
+                         dtype=torch.float32, loc="uniform"),
     # Encoder self-attention: one query per feature pixel.
     "encoder": dict(B=2, Q=None, M=8, D=32, K=4, shapes=pyramid(800, 1333),
                     dtype=torch.float16, loc="refpoint", sigma=0.02, clamp=(-0.1, 1.1)),

@@ -54,6 +54,18 @@ def make_inputs(B, Q, M, D, shapes, K, dtype, device, loc_lo=0.0, loc_hi=1.0, se
     return value, spatial_shapes, starts, loc, attn
 
 
+def per_pixel(grad_loc: torch.Tensor, shapes: torch.Tensor) -> torch.Tensor:
+    """grad_loc (B, Q, M, L, K, 2) divided by each level's (W, H): the
+    gradient with respect to the pixel coordinate.  In fp32 it carries the
+    dot products' rounding (~32 channels, then corner differences) without
+    the factor W that the normalised location adds (up to 167 at the
+    decoder's finest level), so the reference's elementwise 1e-4 applies to
+    it at any map size."""
+    hw = shapes.detach().cpu().double().clamp_min(1.0)  # empty levels: grad_loc is 0
+    wh = torch.stack([hw[:, 1], hw[:, 0]], -1).view(1, 1, 1, -1, 1, 2)
+    return grad_loc.detach().cpu().double() / wh
+
+
 def rel_err(x: torch.Tensor, ref: torch.Tensor) -> float:
     x = x.detach().double().cpu()
     ref = ref.detach().double().cpu()
