@@ -179,6 +179,34 @@ __device__ __forceinline__ void bwd_body(const Params& p, int blk, BwdLds& sm) {
         store_xy<T>(p.grad_loc, pi, r.y, r.z);
       }
     }
+    if constexpr (FUSED) {
+      // Reference-point gradient of the workgroup's queries, when it holds
+      // whole queries (ppb a multiple of M) and one pass holds all their
+      // samples (host-checked): grad_ref = sum over heads and points (and
+      // levels, for one point per query) of grad_offset * (W, H), summed in
+      // a fixed order -- what the separate ref_grad_kernel does from memory.
+      if (p.ref_inline) {
+        const int nl = p.ref_levels ? p.L : 1;
+        const int nqw = ppb / p.M;
+        for (int t = threadIdx.x; t < nqw * nl * 2; t += kBlock) {
+          const int c = t & 1, gi = t >> 1;
+          const int qi = gi / nl, lr = gi - qi * nl;
+          const int pr0 = pair0 + qi * p.M;
+          if (pr0 >= p.npairs) continue;
+          float acc = 0.f;
+          const int l_lo = p.ref_levels ? lr : 0, l_hi = p.ref_levels ? lr + 1 : p.L;
+          for (int l = l_lo; l < l_hi; ++l) {
+            float al = 0.f;
+            for (int m = 0; m < p.M; ++m) {
+              const float4* rr = s_res + (qi * p.M + m) * p.sch + l * p.K;
+              for (int k = 0; k < p.K; ++k) al += c ? rr[k].z : rr[k].y;
+            }
+            acc += al * (c ? (float)lt.h[l] : (float)lt.w[l]);
+          }
+          store1<T>(p.grad_ref, ((uint64_t)(pr0 / p.M) * (uint32_t)nl + (uint32_t)lr) * 2u + c, acc);
+        }
+      }
+    }
     if (pass + 1 < p.npass) __syncthreads();
   }
 }

@@ -243,6 +243,7 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
                      aligned16(grad_value) && owner_plan(d.B, d.Q, d.K, d.D, d.S, d.L, e, &own);
   if (deterministic && !owner && !det_workspace && n_val > 0) return MSDA_ERR_INVALID_ARGUMENT;
   const bool det = deterministic && !owner && n_val > 0;
+  bool ref_inline = false;  // fused: grad_ref formed by the backward workgroups
   // fp32 accumulation is only a separate path for half storage.
   const bool fp32_acc =
       !owner && !det && grad_value_accum != nullptr && dtype != kF32 && n_val > 0;
@@ -280,6 +281,16 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
     const int64_t bs = slice_batch(d);
     if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
     const int64_t ref_per_b = d.Q * (f && f->ref_levels ? d.L : 1) * 2;
+    // Fused, owner path: the gradient workgroups also form grad_ref when
+    // each holds whole queries and all their samples in one pass (then no
+    // ref_grad_kernel launch).
+    if (owner && f && f->grad_ref) {
+      Params t = {};
+      base_params(d, 0, bs, dtype, &t);
+      finish_params(sh, kBwdRecords, &t);
+      const int ppb = (kWave / (sh.g * sh.ts)) * (kBlock / kWave);
+      ref_inline = t.npass == 1 && ppb % d.M == 0;
+    }
     for (int64_t b0 = 0; b0 < d.B; b0 += bs) {
       const int64_t nb = d.B - b0 < bs ? d.B - b0 : bs;
       Params p = {};
@@ -299,6 +310,10 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
       p.det_max = det_max;
       p.det_samples = det_samples;
       if (f) {
+        if (ref_inline) {
+          p.ref_inline = 1;
+          p.grad_ref = at(f->grad_ref, b0 * ref_per_b, e);
+        }
         p.ref = at(f->ref, b0 * ref_per_b, e);
         p.lse = f->lse + b0 * d.Q * d.M;
         p.out_fwd = at(f->output, oo, e);
@@ -356,7 +371,7 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
                                 grad_value, (uint64_t)n_val, st));
     if (rc != MSDA_OK) return rc;
   }
-  if (f && f->grad_ref) {
+  if (f && f->grad_ref && !ref_inline) {
     const int64_t nbq = d.B * d.Q;
     if (compute) {
       Params p = {};

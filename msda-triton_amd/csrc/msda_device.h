@@ -367,6 +367,7 @@ struct Params {
   const void* out_fwd;   // fused backward: the forward output (for <g, out>)
   void* grad_ref;        // fused backward: grad of the reference points
   int32_t ref_levels;    // fused: 1 if reference points are per level
+  int32_t ref_inline;    // fused: the backward workgroups also write grad_ref
   const uint32_t* det_max;  // deterministic: bits of max|A| and max|grad_out| (>= 0)
   float det_samples;        // deterministic: samples per (b, m) = Q * L * K
   uint32_t value_bytes;  // num_records of the value buffer
