@@ -92,17 +92,22 @@ int msda_forward(const void* value, const int64_t* spatial_shapes,
  *                           dtype == MSDA_DTYPE_F32 it may alias grad_value.
  *   grad_sampling_locations (B, Q, M, L, K, 2) dtype, written in full.
  *   grad_attention_weights  (B, Q, M, L, K)    dtype, written in full.
- * The library picks one of three ways to form grad_value
+ * The library picks one of four ways to form grad_value
  * (msda_backward_plan reports which): for few samples per (batch, head,
  * level) -- Q*K <= 2048, a head row of a multiple of 16 bytes up to 256,
  * Q*D*elem <= 40960, 16-byte aligned grad_output and grad_value -- workgroups
  * that own bands of value rows sum each element's contributions in fp32 and
  * store it once (no atomics, no zero-fill, grad_value_accum unused);
- * otherwise grad_value is zero-filled on `stream` and accumulated with
- * atomics, by a kernel that merges samples sharing a row within a workgroup
- * or, for shapes it does not cover, by the direct scatter.  On the owner
+ * otherwise grad_value is zero-filled on `stream` and, for head rows of 32,
+ * 64 or 128 bytes with D a power of two, the samples are binned by band of
+ * value rows (the bins kept in grad_sampling_locations and
+ * grad_attention_weights before those are written) and each band's rows are
+ * summed in fp32 by one workgroup, which stores them, or by several, which
+ * add them with atomics; for other shapes the atomics are issued by a
+ * kernel that merges samples sharing a row within a workgroup or by the
+ * direct scatter.  On the owner
  * path grad_value is bitwise reproducible (each element one fp32 sum in an
- * order fixed by the inputs); on the atomic paths it is not (the order of
+ * order fixed by the inputs); on the binned and atomic paths it is not (the order of
  * the atomics varies).  The other two gradients are reproducible on every
  * path.
  */
@@ -294,6 +299,8 @@ int msda_abi_version(void);
 #define MSDA_BACKWARD_ATOMIC_DIRECT 0 /* zero-fill + direct atomic scatter */
 #define MSDA_BACKWARD_ATOMIC_DEDUP 1  /* zero-fill + row-merging atomic kernel */
 #define MSDA_BACKWARD_OWNER 2         /* row-owner kernel + scatter-free gradient kernel */
+#define MSDA_BACKWARD_BINNED 3        /* zero-fill + samples binned by band of value rows,
+                                         band sums in LDS + scatter-free gradient kernel */
 int msda_backward_plan(int64_t batch, int64_t num_keys, int64_t num_heads, int64_t head_dim,
                        int64_t num_queries, int64_t num_levels, int64_t num_points, int dtype,
                        int deterministic);

@@ -27,7 +27,7 @@ ARCH = "gfx950"
 
 SOURCES = [
     "msda_capi.hip", "msda_forward.hip", "msda_backward.hip", "msda_backward_priv.hip",
-    "msda_backward_owner.hip", "msda_proj.hip",
+    "msda_backward_owner.hip", "msda_backward_binned.hip", "msda_proj.hip",
 ]
 
 # -packed-fp32-ops off: keep v_pk_{add,mul,fma}_f32 out of the device code.

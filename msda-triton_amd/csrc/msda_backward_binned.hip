@@ -1,0 +1,698 @@
+// Binned owner backward: grad_value for calls with many samples per (batch,
+// head, level) -- encoder self-attention, pixel decoders -- formed by the
+// owners of bands of value rows, with plain stores where one workgroup owns
+// a band and few atomics where several share it.
+//
+// Computes the grad_value scatter of the reference's `_msda_backward_kernel`
+// (src/msda_triton/kernels.py:278-291: every in-map corner c of a sample
+// receives A * w_c * grad_out[b, q, m, :]); grad_sampling_locations and
+// grad_attention_weights come from the direct backward kernel without its
+// scatter (msda_backward.hip, NoAcc), launched after these kernels.
+//
+// Per (b, m, level) group, the level's pixels are cut into bands of P rows
+// (P * D fp32 fit in 32 KB of LDS).  A sample's in-map corners lie in
+// [pk, pk + W + 1], pk its first in-map corner, so keying each sample by the
+// band of pk puts every sample that can touch band j in the keys
+// band((j P - W - 1)+) .. j, which are contiguous once the samples are
+// sorted by key.  Four launches:
+//   bin_kernel<count>  per-band sample counts (LDS histogram, one global add
+//                      per band and workgroup);
+//   bin_scan_kernel    per-group exclusive prefix -> each band's first entry
+//                      (the fill cursors), and the work items: each band's
+//                      entry range in chunks of at most `chunk` entries;
+//   bin_kernel<fill>   writes each sample's id (q * K + k) at its band's
+//                      cursor (LDS ranks + one global add per band);
+//   bin_acc_kernel     per work item: the entries' corner contributions to
+//                      the band's rows are summed in LDS (fp32 ds_add), then
+//                      the band is stored (its only item) or added with
+//                      buffer atomics (items of a band split in chunks).
+// No workspace: the entry lists live in grad_sampling_locations (4 bytes per
+// sample, its size at least) and the counts, cursors and items in
+// grad_attention_weights, both written in full afterwards by the gradient
+// kernel.  grad_value (or the fp32 scratch) is zero-filled beforehand.
+// Entry order within a band depends on the global adds' order, so the fp32
+// sums (and grad_value) are not bitwise reproducible; the deterministic
+// entry points do not use this path.
+#include "msda_launch.h"
+
+#include <atomic>
+
+namespace msda {
+
+namespace {
+
+constexpr int kBinPerThread = 4;
+constexpr int kBinPerWg = kBinPerThread * kBlock;  // samples per binning workgroup
+
+// Cell of a sample, as make_sample_at forms it (same clamps): (x, y) is the
+// location, or (FUSED) the offset in level pixels from reference point
+// (rx, ry).
+template <class T, bool FUSED>
+__device__ __forceinline__ void bin_cell(float x, float y, float rx, float ry, float fw, float fh,
+                                         int32_t& x0, int32_t& y0, float& lx, float& ly) {
+  float x0f, y0f;
+  if constexpr (FUSED) {
+    const float xx = __fsub_rn(__fmaf_rn(rx, fw, x), 0.5f);
+    const float yy = __fsub_rn(__fmaf_rn(ry, fh, y), 0.5f);
+    x0f = floorf(xx);
+    y0f = floorf(yy);
+    lx = xx - x0f;
+    ly = yy - y0f;
+  } else {
+    (void)rx;
+    (void)ry;
+    coord_cell<T>(x, fw, x0f, lx);
+    coord_cell<T>(y, fh, y0f, ly);
+  }
+  x0f = fminf(fmaxf(x0f, -2.f), fw + 1.f);
+  y0f = fminf(fmaxf(y0f, -2.f), fh + 1.f);
+  x0 = (int32_t)x0f;
+  y0 = (int32_t)y0f;
+}
+
+// Bit c set when corner c (00, 01, 10, 11) of cell (x0, y0) is in the map.
+__device__ __forceinline__ uint32_t bin_vmask(int32_t x0, int32_t y0, int32_t H, int32_t W) {
+  const bool vx0 = (x0 >= 0) & (x0 < W), vx1 = (x0 >= -1) & (x0 < W - 1);
+  const bool vy0 = (y0 >= 0) & (y0 < H), vy1 = (y0 >= -1) & (y0 < H - 1);
+  return (uint32_t)(vy0 & vx0) | (uint32_t)(vy0 & vx1) << 1 | (uint32_t)(vy1 & vx0) << 2 |
+         (uint32_t)(vy1 & vx1) << 3;
+}
+
+// Buffer views of a call's sample inputs (out-of-range reads give zeros).
+struct BinSrc {
+  __amdgpu_buffer_rsrc_t loc, attn, ref, lse;
+};
+
+__device__ __forceinline__ BinSrc bin_src(const Params& p, const BinArgs& a) {
+  return BinSrc{make_rsrc(p.loc, a.loc_bytes), make_rsrc(p.attn, a.attn_bytes),
+                make_rsrc(p.ref, p.ref_bytes), make_rsrc(p.lse, (uint32_t)p.npairs * 4u)};
+}
+
+template <class T>
+__device__ __forceinline__ void bin_xy(__amdgpu_buffer_rsrc_t r, uint32_t i, float& x, float& y) {
+  if constexpr (T::kBytes == 4) {
+    const i32x2 xy = __builtin_amdgcn_raw_buffer_load_b64(r, i * 8u, 0, 0);
+    x = __int_as_float(xy[0]);
+    y = __int_as_float(xy[1]);
+  } else {
+    unpack2<T>((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, 0), x, y);
+  }
+}
+
+template <class T>
+__device__ __forceinline__ float bin_one(__amdgpu_buffer_rsrc_t r, uint32_t i) {
+  if constexpr (T::kBytes == 4) {
+    return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, 0));
+  } else {
+    return unpack1<T>((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, i * 2u, 0, 0));
+  }
+}
+
+// Raw inputs of one sample: location (or offset), weight (or logit), and
+// for FUSED the reference point and the pair's log-sum-exp.
+struct BinIn {
+  float x, y, a, rx, ry, lse;
+};
+
+template <class T, bool FUSED, bool kWeight>
+__device__ __forceinline__ BinIn bin_load(const Params& p, const BinSrc& rs, uint32_t bq,
+                                          uint32_t pair, uint32_t pi, uint32_t l) {
+  BinIn r;
+  bin_xy<T>(rs.loc, pi, r.x, r.y);
+  r.a = kWeight ? bin_one<T>(rs.attn, pi) : 0.f;
+  r.rx = r.ry = r.lse = 0.f;
+  if constexpr (FUSED) {
+    bin_xy<T>(rs.ref, p.ref_levels ? bq * (uint32_t)p.L + l : bq, r.rx, r.ry);
+    if constexpr (kWeight)
+      r.lse = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs.lse, pair * 4u, 0, 0));
+  }
+  return r;
+}
+
+// Exclusive prefix sum over the workgroup (Hillis-Steele in `s`); `total`
+// receives the sum.  Every thread must call it.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* s, uint32_t& total) {
+  s[threadIdx.x] = v;
+  __syncthreads();
+  for (int d = 1; d < kBlock; d <<= 1) {
+    const uint32_t x = (int)threadIdx.x >= d ? s[threadIdx.x - d] : 0u;
+    __syncthreads();
+    s[threadIdx.x] += x;
+    __syncthreads();
+  }
+  total = s[kBlock - 1];
+  const uint32_t incl = s[threadIdx.x];
+  __syncthreads();
+  return incl - v;
+}
+
+struct GroupLevel {
+  int32_t b, m, l, H, W, st, nb, nk;  // nb bands of 2^log2p pixels, nk keys of 2^log2k
+};
+
+__device__ __forceinline__ GroupLevel group_level(const Params& p, const BinArgs& a, int g) {
+  GroupLevel r;
+  r.l = g % p.L;
+  const int bm = g / p.L;
+  r.m = bm % p.M;
+  r.b = bm / p.M;
+  r.H = (int32_t)p.shapes[2 * r.l];
+  r.W = (int32_t)p.shapes[2 * r.l + 1];
+  r.st = (int32_t)p.starts[r.l];
+  const int64_t hw = (int64_t)r.H * r.W;
+  const int64_t nk = (hw + (1 << a.log2k) - 1) >> a.log2k;
+  const bool bad = hw < 0 || nk > a.nbmax;  // the group is skipped
+  r.nk = bad ? -1 : (int32_t)nk;
+  r.nb = bad ? -1 : (int32_t)((hw + (1 << a.log2p) - 1) >> a.log2p);
+  return r;
+}
+
+// FILL == false: per-band counts; true: entries at the band cursors.
+template <class T, bool FUSED, bool FILL>
+__global__ __launch_bounds__(kBlock) void bin_kernel(Params p, BinArgs a) {
+  __shared__ uint32_t s_hist[kBinMaxBands];
+  __shared__ uint32_t s_base[FILL ? kBinMaxBands : 1];
+  const int g = blockIdx.x / a.nqb;
+  const int qb = blockIdx.x - g * a.nqb;
+  const GroupLevel gl = group_level(p, a, g);
+  if (gl.nk <= 0) return;
+  for (int j = threadIdx.x; j < gl.nk; j += kBlock) s_hist[j] = 0u;
+  __syncthreads();
+
+  const uint32_t qk = (uint32_t)(p.Q * p.K);
+  const BinSrc rs = bin_src(p, a);
+  const float fw = (float)gl.W, fh = (float)gl.H;
+  uint32_t key[kBinPerThread], rank[kBinPerThread], lid[kBinPerThread];
+#pragma unroll
+  for (int u = 0; u < kBinPerThread; ++u) {
+    const uint32_t li = (uint32_t)qb * kBinPerWg + u * kBlock + threadIdx.x;
+    lid[u] = li;
+    key[u] = ~0u;
+    rank[u] = 0u;
+    if (li < qk) {
+      const uint32_t q = fdiv(li, p.div_k), k = li - q * (uint32_t)p.K;
+      const uint32_t bq = (uint32_t)gl.b * p.Q + q;
+      const uint32_t pair = bq * p.M + gl.m;
+      const uint32_t pi = pair * (uint32_t)p.LK + (uint32_t)gl.l * p.K + k;
+      const BinIn in = bin_load<T, FUSED, false>(p, rs, bq, pair, pi, gl.l);
+      int32_t x0, y0;
+      float lx, ly;
+      bin_cell<T, FUSED>(in.x, in.y, in.rx, in.ry, fw, fh, x0, y0, lx, ly);
+      const uint32_t vm = bin_vmask(x0, y0, gl.H, gl.W);
+      if (vm) {
+        const int32_t c = __builtin_ctz(vm);
+        const int32_t pk = y0 * gl.W + x0 + ((c & 1) ? 1 : 0) + ((c & 2) ? gl.W : 0);
+        key[u] = (uint32_t)pk >> a.log2k;
+        rank[u] = atomicAdd(&s_hist[key[u]], 1u);
+      }
+    }
+  }
+  __syncthreads();
+  uint32_t* const counts = (FILL ? a.cursors : a.counts) + (uint32_t)g * a.nbmax;
+  for (int j = threadIdx.x; j < gl.nk; j += kBlock) {
+    const uint32_t h = s_hist[j];
+    if (h == 0u) continue;
+    if constexpr (FILL) {
+      s_base[j] = atomicAdd(&counts[j], h);
+    } else {
+      atomicAdd(&counts[j], h);
+    }
+  }
+  if constexpr (FILL) {
+    __syncthreads();
+    uint32_t* const ent = a.entries + (uint64_t)g * qk;
+#pragma unroll
+    for (int u = 0; u < kBinPerThread; ++u) {
+      if (key[u] != ~0u) {
+        const uint32_t pos = s_base[key[u]] + rank[u];
+        if (pos < qk) ent[pos] = lid[u];
+      }
+    }
+  }
+}
+
+// One workgroup per group: cursors = exclusive prefix of the counts, then
+// the work items (band | several << 31, first entry, end entry, 0).
+__global__ __launch_bounds__(kBlock) void bin_scan_kernel(Params p, BinArgs a) {
+  __shared__ uint32_t s_off[kBinMaxBands + 1];
+  __shared__ uint32_t s_scan[kBlock];
+  const int g = blockIdx.x;
+  const GroupLevel gl = group_level(p, a, g);
+  if (gl.nk <= 0) {
+    if (threadIdx.x == 0) a.nitems[g] = 0u;
+    return;
+  }
+  const uint32_t* counts = a.counts + (uint32_t)g * a.nbmax;
+  uint32_t* cursors = a.cursors + (uint32_t)g * a.nbmax;
+  uint32_t carry = 0u, total = 0u;
+  for (int j0 = 0; j0 < gl.nk; j0 += kBlock) {
+    const int j = j0 + threadIdx.x;
+    const uint32_t v = j < gl.nk ? counts[j] : 0u;
+    const uint32_t ex = block_excl_scan(v, s_scan, total);
+    if (j < gl.nk) {
+      s_off[j] = carry + ex;
+      cursors[j] = carry + ex;
+    }
+    carry += total;
+  }
+  if (threadIdx.x == 0) s_off[gl.nk] = carry;
+  __syncthreads();
+
+  // Band j (pixels [jP, jP + P)) takes the samples keyed from pixel
+  // jP - W - 1 (their last corner is at most W + 1 past the key pixel) to
+  // its last pixel: keys lo_key(j) .. hi_key(j), contiguous entries.
+  const int64_t hw = (int64_t)gl.H * gl.W;
+  auto range = [&](int j, uint32_t& lo, uint32_t& hi) {
+    const int64_t p0 = ((int64_t)j << a.log2p) - (int64_t)gl.W - 1;
+    const int64_t p1 = ((int64_t)(j + 1) << a.log2p) < hw ? ((int64_t)(j + 1) << a.log2p) : hw;
+    lo = s_off[p0 <= 0 ? 0 : (int)(p0 >> a.log2k)];
+    hi = s_off[(int)((p1 - 1) >> a.log2k) + 1];
+  };
+  uint32_t vis = 0u;
+  for (int j = threadIdx.x; j < gl.nb; j += kBlock) {
+    uint32_t lo, hi;
+    range(j, lo, hi);
+    vis += hi - lo;
+  }
+  uint32_t vtot = 0u;
+  (void)block_excl_scan(vis, s_scan, vtot);
+  const uint32_t room = (uint32_t)(a.cap - gl.nb);  // > 0 (host: cap > bands per level)
+  uint32_t ceff = (vtot + room - 1u) / room;
+  if (ceff < (uint32_t)a.chunk) ceff = (uint32_t)a.chunk;
+
+  uint4* items = a.items + (uint32_t)g * a.cap;
+  uint32_t ibase = 0u;
+  for (int j0 = 0; j0 < gl.nb; j0 += kBlock) {
+    const int j = j0 + threadIdx.x;
+    uint32_t lo = 0u, hi = 0u, nch = 0u;
+    if (j < gl.nb) {
+      range(j, lo, hi);
+      nch = (hi - lo + ceff - 1u) / ceff;
+    }
+    const uint32_t ex = block_excl_scan(nch, s_scan, total);
+    for (uint32_t c = 0; c < nch; ++c) {
+      const uint32_t e0 = lo + c * ceff;
+      const uint32_t e1 = hi - e0 > ceff ? e0 + ceff : hi;
+      const uint32_t idx = ibase + ex + c;
+      if (idx < (uint32_t)a.cap)
+        items[idx] = make_uint4((uint32_t)j | (nch > 1u ? 0x80000000u : 0u), e0, e1, 0u);
+    }
+    ibase += total;
+  }
+  if (threadIdx.x == 0) a.nitems[g] = ibase < (uint32_t)a.cap ? ibase : (uint32_t)a.cap;
+}
+
+// Per work item: sum the entries' contributions to the band's rows in LDS,
+// then store or add them.  Each round of 256 staged samples is sorted by
+// band row in LDS (integer counts, prefix, fill); every thread owns 32
+// fp32 accumulators (32 channels of one row, or all channels of several) in
+// registers for the whole item and adds its rows' entries to them -- no
+// float atomics, no read-modify-write of LDS.  The sums leave through LDS so
+// that the stores (or atomics) cover whole rows.  RB = D * sizeof(T) bytes
+// of a grad_out row.  A: the element type of the target (T, or F32 for the fp32
+// scratch).  Persistent: workgroup w takes items w, w + grid, ... of the
+// flattened list, so every workgroup's loop ends.
+template <class T, class A, int RB, bool FUSED>
+__global__ __launch_bounds__(kBlock, 3) void bin_acc_kernel(Params p, BinArgs a) {
+  constexpr int kD = RB / T::kBytes;  // channels
+  constexpr int kQ = RB / 16;         // 16-byte pieces of a grad_out row
+  constexpr int kStride = kD + 1;     // LDS row stride (floats): spreads teams over banks
+  static_assert(kD <= kWave && (kD & (kD - 1)) == 0, "team of D lanes");
+  constexpr int kP = kBinAccFloats / kD;  // rows per band
+  constexpr int kPerT = (kP + kBlock - 1) / kBlock;
+  // Thread-owned accumulators: kChT channels of kRowsT rows (32 floats);
+  // 8 channels each, so that the entries of a busy row are split over
+  // several threads.
+  constexpr int kChT = kD < 8 ? kD : 8;
+  constexpr int kTpr = kD / kChT;                // threads per row
+  constexpr int kRowsT = kP * kTpr / kBlock;     // rows per thread
+  constexpr int kRowStep = kBlock / kTpr;
+  static_assert(kRowsT * kChT == kBinAccFloats / kBlock, "32 accumulators per thread");
+  // grad_out rows (raw) during the rounds; the band's sums at the end.
+  constexpr int kUnion16 = (kP * kStride * 4 > kBlock * RB ? kP * kStride * 4 : kBlock * RB) / 16;
+  __shared__ i32x4 s_u[kUnion16];
+  i32x4* const s_g = s_u;
+  float* const s_acc = reinterpret_cast<float*>(s_u);
+  __shared__ float4 s_coef[kBlock];   // A * w_c
+  __shared__ uint32_t s_cnt[kP];      // corner entries per band row (this round)
+  __shared__ uint32_t s_off[kP + 1];  // their exclusive prefix
+  __shared__ uint16_t s_ent[4 * kBlock];  // entries by row: staged sample * 4 + corner
+  __shared__ uint32_t s_wsum[kBlock / kWave];
+  __shared__ uint32_t s_pre[kBinMaxGroups + 1];
+  __shared__ uint32_t s_scan[kBlock];
+  for (int i = threadIdx.x; i < kP; i += kBlock) s_cnt[i] = 0u;
+
+  // Item prefix over the groups.
+  {
+    constexpr int kPer = kBinMaxGroups / kBlock;
+    uint32_t v[kPer], sum = 0u, total = 0u;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int gi = threadIdx.x * kPer + i;
+      v[i] = gi < a.ngroups ? a.nitems[gi] : 0u;
+      sum += v[i];
+    }
+    uint32_t ex = block_excl_scan(sum, s_scan, total);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int gi = threadIdx.x * kPer + i;
+      if (gi < a.ngroups) s_pre[gi] = ex;
+      ex += v[i];
+    }
+    if (threadIdx.x == 0) s_pre[a.ngroups] = total;
+    __syncthreads();
+  }
+  const uint32_t ntot = s_pre[a.ngroups];
+  const uint32_t qk = (uint32_t)(p.Q * p.K);
+  const uint32_t P = 1u << a.log2p;
+  const BinSrc rs = bin_src(p, a);
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.grad_out, p.gout_bytes);
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.grad_acc, p.acc_bytes);
+
+  for (uint32_t w = blockIdx.x; w < ntot; w += gridDim.x) {
+    int lo = 0, hi = a.ngroups;  // s_pre[lo] <= w < s_pre[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_pre[mid] <= w) lo = mid; else hi = mid;
+    }
+    const int g = lo;
+    const uint4 it = a.items[(uint32_t)g * a.cap + (w - s_pre[g])];
+    const GroupLevel gl = group_level(p, a, g);
+    const uint32_t band = it.x & 0x7fffffffu;
+    const bool several = (it.x >> 31) != 0u;
+    const uint32_t e0 = it.y, e1 = it.z < qk ? it.z : qk;
+    const int32_t r0 = (int32_t)(band << a.log2p);
+    const int32_t hw = gl.H * gl.W;
+    const int32_t nrow = hw - r0 < (int32_t)P ? hw - r0 : (int32_t)P;
+    const float fw = (float)gl.W, fh = (float)gl.H;
+    const uint32_t* ent = a.entries + (uint64_t)g * qk;
+    float acc[kRowsT][kChT];
+#pragma unroll
+    for (int i = 0; i < kRowsT; ++i)
+#pragma unroll
+      for (int k = 0; k < kChT; ++k) acc[i][k] = 0.f;
+    const int own_r0 = threadIdx.x / kTpr, own_c0 = (threadIdx.x % kTpr) * kChT;
+
+    // Software pipeline: entry ids two rounds ahead, parameters and
+    // grad_out rows one round ahead of the round being added.
+    auto load_id = [&](uint32_t e) { return e < e1 ? ent[e] : ~0u; };
+    struct Pre {
+      uint32_t ok;
+      BinIn in;
+      i32x4 g[kQ];
+    };
+    auto load_pre = [&](uint32_t li, Pre& s) {
+      s.ok = li < qk;
+      s.in = BinIn{0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (s.ok) {
+        const uint32_t q = fdiv(li, p.div_k), k = li - q * (uint32_t)p.K;
+        const uint32_t bq = (uint32_t)gl.b * p.Q + q;
+        const uint32_t pair = bq * p.M + gl.m;
+        const uint32_t pi = pair * (uint32_t)p.LK + (uint32_t)gl.l * p.K + k;
+        s.in = bin_load<T, FUSED, true>(p, rs, bq, pair, pi, gl.l);
+#pragma unroll
+        for (int i = 0; i < kQ; ++i)
+          s.g[i] = __builtin_amdgcn_raw_buffer_load_b128(rg, pair * (uint32_t)RB + 16u * i, 0, 0);
+      }
+    };
+    Pre cur;
+    load_pre(load_id(e0 + threadIdx.x), cur);
+    uint32_t id_next = load_id(e0 + kBlock + threadIdx.x);
+    for (uint32_t rb = e0; rb < e1; rb += kBlock) {
+      // Stage this round's samples; count their corner entries per row
+      // (the returned count is the entry's rank in its row).
+      uint32_t rw[4] = {0xffffu, 0xffffu, 0xffffu, 0xffffu}, rk[4] = {0u, 0u, 0u, 0u};
+      float4 cf = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (cur.ok) {
+        int32_t x0, y0;
+        float lx, ly;
+        bin_cell<T, FUSED>(cur.in.x, cur.in.y, cur.in.rx, cur.in.ry, fw, fh, x0, y0, lx, ly);
+        const uint32_t vm = bin_vmask(x0, y0, gl.H, gl.W);
+        const int32_t base = y0 * gl.W + x0 - r0;
+        const int32_t rr[4] = {base, base + 1, base + gl.W, base + gl.W + 1};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (((vm >> c) & 1u) && rr[c] >= 0 && rr[c] < nrow) {
+            rw[c] = (uint32_t)rr[c];
+            rk[c] = atomicAdd(&s_cnt[rw[c]], 1u);
+          }
+        }
+        const float mx = 1.f - lx, my = 1.f - ly;
+        const float aw = FUSED ? expf(cur.in.a - cur.in.lse) : cur.in.a;
+        cf = make_float4(aw * (mx * my), aw * (lx * my), aw * (mx * ly), aw * (lx * ly));
+      }
+      s_coef[threadIdx.x] = cf;
+#pragma unroll
+      for (int i = 0; i < kQ; ++i) s_g[threadIdx.x * kQ + i] = cur.g[i];
+      // Next round's loads, in flight while this round is summed.
+      load_pre(id_next, cur);
+      id_next = load_id(rb + 2 * kBlock + threadIdx.x);
+      __syncthreads();
+
+      // Row offsets: exclusive prefix of the counts (which are reset).
+      {
+        uint32_t v[kPerT], sum = 0u;
+#pragma unroll
+        for (int i = 0; i < kPerT; ++i) {
+          const int r = threadIdx.x * kPerT + i;
+          v[i] = r < kP ? s_cnt[r] : 0u;
+          if (r < kP) s_cnt[r] = 0u;
+          sum += v[i];
+        }
+        const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+        uint32_t x = sum;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+          const uint32_t y = (uint32_t)__shfl_up((int)x, d);
+          if (lane >= d) x += y;
+        }
+        if (lane == kWave - 1) s_wsum[wv] = x;
+        __syncthreads();
+        uint32_t ex = x - sum, tot = 0u;
+#pragma unroll
+        for (int w2 = 0; w2 < kBlock / kWave; ++w2) {
+          const uint32_t ws = s_wsum[w2];
+          if (w2 < wv) ex += ws;
+          tot += ws;
+        }
+#pragma unroll
+        for (int i = 0; i < kPerT; ++i) {
+          const int r = threadIdx.x * kPerT + i;
+          if (r < kP) s_off[r] = ex;
+          ex += v[i];
+        }
+        if (threadIdx.x == 0) s_off[kP] = tot;
+        __syncthreads();
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (rw[c] != 0xffffu) s_ent[s_off[rw[c]] + rk[c]] = (uint16_t)(threadIdx.x * 4 + c);
+      __syncthreads();
+
+      // Each thread adds the entries of the rows it owns to its registers.
+      const float* coefs = reinterpret_cast<const float*>(s_coef);
+#pragma unroll
+      for (int i = 0; i < kRowsT; ++i) {
+        const int r = own_r0 + i * kRowStep;
+        const uint32_t eb = s_off[r], ee = s_off[r + 1];
+        constexpr int kW = kChT * T::kBytes / 16;  // 16-byte pieces of this thread's channels
+        const int q0 = own_c0 * T::kBytes / 16;
+        auto add = [&](float c, const i32x4 (&x)[kW]) {
+#pragma unroll
+          for (int w = 0; w < kW; ++w) {
+            if constexpr (T::kBytes == 4) {
+#pragma unroll
+              for (int k = 0; k < 4; ++k) acc[i][4 * w + k] += c * __int_as_float(x[w][k]);
+            } else {
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                float lo, hi;
+                unpack2<T>((uint32_t)x[w][k], lo, hi);
+                acc[i][8 * w + 2 * k] += c * lo;
+                acc[i][8 * w + 2 * k + 1] += c * hi;
+              }
+            }
+          }
+        };
+        uint32_t e = eb;
+        for (; e + 4 <= ee; e += 4) {  // four entries' loads in flight together
+          uint32_t u[4];
+          float c[4];
+          i32x4 x[4][kW];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) u[j] = s_ent[e + j];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            c[j] = coefs[u[j]];
+#pragma unroll
+            for (int w = 0; w < kW; ++w) x[j][w] = s_g[(u[j] >> 2) * kQ + q0 + w];
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) add(c[j], x[j]);
+        }
+        for (; e < ee; ++e) {
+          const uint32_t u = s_ent[e];
+          i32x4 x[kW];
+#pragma unroll
+          for (int w = 0; w < kW; ++w) x[w] = s_g[(u >> 2) * kQ + q0 + w];
+          add(coefs[u], x);
+        }
+      }
+      __syncthreads();
+    }
+
+    // Accumulators to LDS (rows exclusive to their threads), then out.
+#pragma unroll
+    for (int i = 0; i < kRowsT; ++i)
+#pragma unroll
+      for (int k = 0; k < kChT; ++k) s_acc[(own_r0 + i * kRowStep) * kStride + own_c0 + k] = acc[i][k];
+    __syncthreads();
+
+    // The band's rows: value rows st + r0 + row of (b, m).
+    const uint32_t vrow0 = (((uint32_t)gl.b * p.S + gl.st + r0) * p.M + gl.m) * (uint32_t)kD;
+    const uint32_t vstep = (uint32_t)p.M * kD;
+    for (int idx = 2 * threadIdx.x; idx < nrow * kD; idx += 2 * kBlock) {
+      const int row = idx / kD, c0 = idx % kD;
+      const float v0 = s_acc[row * kStride + c0], v1 = s_acc[row * kStride + c0 + 1];
+      const uint32_t el = vrow0 + (uint32_t)row * vstep + c0;
+      if (!several) {
+        if constexpr (A::kBytes == 4) {
+          __builtin_amdgcn_raw_buffer_store_b64(i32x2{__float_as_int(v0), __float_as_int(v1)}, rc,
+                                                el * 4u, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b32((int)pack2<A>(v0, v1), rc, el * 2u, 0, 0);
+        }
+      } else if (v0 != 0.f || v1 != 0.f) {
+        if constexpr (A::kBytes == 4) {
+          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v0, rc, (int)(el * 4u), 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v1, rc, (int)(el * 4u + 4u), 0, 0);
+        } else if constexpr (A::kCode == kBF16) {
+          raw_buffer_atomic_fadd_v2bf16(bf16x2{(__bf16)v0, (__bf16)v1}, rc, (int)(el * 2u), 0, 0);
+        } else {
+          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_v2f16(f16x2{(_Float16)v0, (_Float16)v1}, rc,
+                                                            (int)(el * 2u), 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+int bin_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+template <class T, class A, bool FUSED>
+hipError_t launch_acc(int rb, const Params& p, const BinArgs& a, hipStream_t st) {
+  const int64_t slots = (int64_t)a.ngroups * a.cap;
+  const int64_t want = 3 * (int64_t)bin_cus();
+  const dim3 grid((unsigned)(slots < want ? slots : want));
+  switch (rb) {
+    case 32:
+      hipLaunchKernelGGL((bin_acc_kernel<T, A, 32, FUSED>), grid, dim3(kBlock), 0, st, p, a);
+      break;
+    case 64:
+      hipLaunchKernelGGL((bin_acc_kernel<T, A, 64, FUSED>), grid, dim3(kBlock), 0, st, p, a);
+      break;
+    case 128:
+      hipLaunchKernelGGL((bin_acc_kernel<T, A, 128, FUSED>), grid, dim3(kBlock), 0, st, p, a);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <class T, bool FUSED>
+hipError_t launch_t(bool f32acc, const Params& p, const BinArgs& a, hipStream_t st) {
+  const int ng = a.ngroups;
+  hipError_t e = launch_zero(a.counts, (uint64_t)ng * a.nbmax * 4u, st);
+  if (e != hipSuccess) return e;
+  const dim3 gbin((unsigned)(ng * a.nqb));
+  hipLaunchKernelGGL((bin_kernel<T, FUSED, false>), gbin, dim3(kBlock), 0, st, p, a);
+  hipLaunchKernelGGL(bin_scan_kernel, dim3((unsigned)ng), dim3(kBlock), 0, st, p, a);
+  hipLaunchKernelGGL((bin_kernel<T, FUSED, true>), gbin, dim3(kBlock), 0, st, p, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int rb = p.D * T::kBytes;
+  if constexpr (T::kBytes == 4) {
+    (void)f32acc;
+    return launch_acc<T, F32, FUSED>(rb, p, a, st);
+  } else {
+    return f32acc ? launch_acc<T, F32, FUSED>(rb, p, a, st) : launch_acc<T, T, FUSED>(rb, p, a, st);
+  }
+}
+
+}  // namespace
+
+bool bin_plan(int64_t B, int64_t Q, int64_t M, int64_t K, int64_t D, int64_t S, int64_t L,
+              int elem_bytes, void* grad_loc, void* grad_attn, BinArgs* a) {
+  const int64_t rb = D * elem_bytes;
+  if (rb != 32 && rb != 64 && rb != 128) return false;
+  if (D > kWave || (D & (D - 1)) != 0) return false;
+  const int64_t qk = Q * K;
+  if (qk <= 0 || S <= 0 || L <= 0 || B <= 0 || M <= 0) return false;
+  const int64_t ng = B * M * L;
+  if (ng > kBinMaxGroups) return false;
+  int log2p = 0;
+  while ((int64_t)2 << log2p <= kBinAccFloats / D) ++log2p;  // P = 2^log2p <= 8192 / D
+  const int64_t P = (int64_t)1 << log2p;
+  // Keys of 32 pixels (coarser for very large maps): a band reads the keys
+  // of its own pixels and of the W + 1 before it.
+  int log2k = 5;
+  while (log2k < log2p && (S >> log2k) + 2 > kBinMaxBands) ++log2k;
+  const int64_t nbmax = (S >> log2k) + 2;  // keys per level, at most
+  if (nbmax > kBinMaxBands) return false;
+  const int64_t bands = (S + P - 1) / P + 1;
+  const int64_t cap = bands + (2 * qk + kBinChunk - 1) / kBinChunk + 16;
+  // Entries: 4 bytes per sample in grad_loc (2 * elem_bytes per sample).
+  if ((reinterpret_cast<uintptr_t>(grad_loc) & 3u) != 0) return false;
+  // Counts, cursors, item counts, then 16-byte aligned items in grad_attn.
+  uintptr_t base = reinterpret_cast<uintptr_t>(grad_attn);
+  if ((base & 3u) != 0) return false;
+  const uint64_t avail = (uint64_t)(ng * qk * elem_bytes);
+  const uint64_t n_cnt = (uint64_t)(ng * nbmax) * 4u;
+  uint64_t off_items = 2 * n_cnt + (uint64_t)ng * 4u;
+  off_items += (16u - ((base + off_items) & 15u)) & 15u;
+  const uint64_t need = off_items + (uint64_t)(ng * cap) * 16u;
+  if (need > avail || (uint64_t)(ng * qk * 2 * elem_bytes) > 0xffffffffull) return false;
+  char* ws = static_cast<char*>(grad_attn);
+  a->entries = static_cast<uint32_t*>(grad_loc);
+  a->counts = reinterpret_cast<uint32_t*>(ws);
+  a->cursors = reinterpret_cast<uint32_t*>(ws + n_cnt);
+  a->nitems = reinterpret_cast<uint32_t*>(ws + 2 * n_cnt);
+  a->items = reinterpret_cast<uint4*>(ws + off_items);
+  a->ngroups = (int32_t)ng;
+  a->nbmax = (int32_t)nbmax;
+  a->cap = (int32_t)cap;
+  a->nqb = (int32_t)((qk + kBinPerWg - 1) / kBinPerWg);
+  a->log2p = log2p;
+  a->log2k = log2k;
+  a->chunk = kBinChunk;
+  a->loc_bytes = (uint32_t)(ng * qk * 2 * elem_bytes);
+  a->attn_bytes = (uint32_t)(ng * qk * elem_bytes);
+  return true;
+}
+
+hipError_t launch_binned(int dtype, bool fused, bool f32acc, const Params& p, const BinArgs& a,
+                         hipStream_t st) {
+  if (a.ngroups <= 0) return hipSuccess;
+  switch (dtype) {
+    case kF32: return fused ? launch_t<F32, true>(false, p, a, st) : launch_t<F32, false>(false, p, a, st);
+    case kF16: return fused ? launch_t<F16, true>(f32acc, p, a, st) : launch_t<F16, false>(f32acc, p, a, st);
+    case kBF16:
+      return fused ? launch_t<BF16, true>(f32acc, p, a, st) : launch_t<BF16, false>(f32acc, p, a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace msda

@@ -98,6 +98,10 @@ static bool bwd_priv_enabled() {
 static bool bwd_owner_enabled() {
   return getenv("MSDA_BWD_OWNER") == nullptr || env_int("MSDA_BWD_OWNER") != 0;
 }
+// MSDA_BWD_BIN=0: no binned owner path (the atomic kernels instead).
+static bool bwd_bin_enabled() {
+  return getenv("MSDA_BWD_BIN") == nullptr || env_int("MSDA_BWD_BIN") != 0;
+}
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 static int elem_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
@@ -247,6 +251,20 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
   // fp32 accumulation is only a separate path for half storage.
   const bool fp32_acc =
       !owner && !det && grad_value_accum != nullptr && dtype != kF32 && n_val > 0;
+  // Binned owner path (many samples per (b, m, level)): every slice's
+  // grad_loc / grad_attn must hold its bookkeeping (bin_plan).
+  bool binned = false;
+  if (compute && !owner && !deterministic && bwd_bin_enabled()) {
+    const int64_t bs0 = slice_batch(d);
+    binned = bs0 > 0;
+    for (int64_t b0 = 0; binned && b0 < d.B; b0 += bs0) {
+      const int64_t nb = d.B - b0 < bs0 ? d.B - b0 : bs0;
+      const int64_t so = b0 * d.Q * d.M * d.L * d.K;
+      BinArgs ba;
+      binned = bin_plan(nb, d.Q, d.M, d.K, d.D, d.S, d.L, e, at(grad_loc, so * 2, e),
+                        at(grad_attn, so, e), &ba);
+    }
+  }
   const AccMode mode = det ? kAccI64 : fp32_acc ? kAccF32 : kAccNative;
   void* acc = det ? det_workspace : fp32_acc ? static_cast<void*>(grad_value_accum) : grad_value;
   const int acc_e = det ? 8 : fp32_acc ? 4 : e;
@@ -271,12 +289,13 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
     if (rc == MSDA_OK) rc = status(launch_zero(grad_attn, (uint64_t)(n_smp * e), st));
     if (rc != MSDA_OK) return rc;
   } else if (compute) {
-    // The owner path runs the direct kernel without its scatter: no atomics
+    // The owner paths run the direct kernel without its scatter: no atomics
     // to spread over pairs, so it takes the forward's launch shape.
+    const bool no_scatter = owner || binned;
     Shape sh;
-    if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, !owner,
-                      owner ? fwd_ts_pref() : bwd_ts_pref(),
-                      owner ? fwd_cb_pref() : bwd_cb_pref(), &sh))
+    if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, !no_scatter,
+                      no_scatter ? fwd_ts_pref() : bwd_ts_pref(),
+                      no_scatter ? fwd_cb_pref() : bwd_cb_pref(), &sh))
       return MSDA_ERR_UNSUPPORTED_SHAPE;
     const int64_t bs = slice_batch(d);
     if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
@@ -318,6 +337,18 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
         p.lse = f->lse + b0 * d.Q * d.M;
         p.out_fwd = at(f->output, oo, e);
         p.ref_levels = f->ref_levels;
+      }
+      if (binned) {
+        BinArgs ba;
+        if (!bin_plan(nb, d.Q, d.M, d.K, d.D, d.S, d.L, e, p.grad_loc, p.grad_attn, &ba))
+          return MSDA_ERR_LAUNCH;  // checked for every slice above
+        if (f) p.ref_bytes = (uint32_t)(nb * ref_per_b * e);
+        finish_params(sh, kBwdRecords, &p);
+        rc = status(launch_binned(dtype, f != nullptr, fp32_acc, p, ba, st));
+        // grad_loc / grad_attn (their bookkeeping contents overwritten).
+        if (rc == MSDA_OK) rc = status(launch_backward(dtype, kAccNone, f != nullptr, sh, p, st));
+        if (rc != MSDA_OK) return rc;
+        continue;
       }
       if (owner) {
         Params po = p;
@@ -691,9 +722,13 @@ extern "C" int msda_backward_plan(int64_t batch, int64_t num_keys, int64_t num_h
   const bool compute = d.B * d.Q * d.M * d.L * d.K > 0 && d.B * d.Q * d.M * d.D > 0 && d.S > 0;
   Params own = {};
   base_params(d, 0, d.B, dtype, &own);
-  (void)deterministic;  // the owner path serves both modes
   if (compute && bwd_owner_enabled() && owner_plan(d.B, d.Q, d.K, d.D, d.S, d.L, e, &own))
     return MSDA_BACKWARD_OWNER;
+  const int64_t bs = slice_batch(d);
+  BinArgs ba;
+  if (compute && !deterministic && bwd_bin_enabled() && bs > 0 &&
+      bin_plan(bs < d.B ? bs : d.B, d.Q, d.M, d.K, d.D, d.S, d.L, e, nullptr, nullptr, &ba))
+    return MSDA_BACKWARD_BINNED;
   Shape sh;
   if (compute && !choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, true,
                                bwd_ts_pref(), bwd_cb_pref(), &sh))

@@ -56,6 +56,31 @@ bool owner_plan(int64_t B, int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L
 // workgroups computing grad_loc / grad_attn (params pd, runtime shape).
 hipError_t launch_owner(int dtype, bool fused, const Params& p, const Params& pd,
                         hipStream_t st);
+// Binned owner backward (msda_backward_binned.hip): grad_value for calls
+// with many samples per (b, m, level), summed per band of value rows in LDS.
+// Its bookkeeping lives in the call's grad_loc / grad_attn buffers, which
+// the gradient kernel overwrites afterwards.
+constexpr int kBinAccFloats = 8192;  // fp32 band accumulator: P * D floats (32 KB)
+constexpr int kBinMaxBands = 4096;   // bands per level
+constexpr int kBinMaxGroups = 1024;  // (b, m, level) groups per launch
+constexpr int kBinChunk = 2048;      // entries per work item (at least)
+struct BinArgs {
+  uint32_t* entries;  // [group][Q*K] sample ids q*K + k, by band (in grad_loc)
+  uint32_t* counts;   // [group][nbmax] samples keyed to each key (2^log2k pixels)
+  uint32_t* cursors;  // [group][nbmax] first entry of each key, then fill cursor
+  uint32_t* nitems;   // [group] work items
+  uint4* items;       // [group][cap] (band | split << 31, first entry, end entry, 0)
+  uint32_t loc_bytes, attn_bytes;
+  int32_t ngroups, nbmax, cap, nqb, log2p, log2k, chunk;  // bands of 2^log2p pixels
+};
+// Fills `a` for a slice of B batches; false when the shapes or the buffers
+// (size, alignment) do not suit the path.  NULL buffers: shape check only.
+bool bin_plan(int64_t B, int64_t Q, int64_t M, int64_t K, int64_t D, int64_t S, int64_t L,
+              int elem_bytes, void* grad_loc, void* grad_attn, BinArgs* a);
+// Zeroes the counts and runs the four kernels; grad_value (p.grad_acc, of
+// element type fp32 when f32acc or dtype is fp32) must be zero on entry.
+hipError_t launch_binned(int dtype, bool fused, bool f32acc, const Params& p, const BinArgs& a,
+                         hipStream_t st);
 // Fused front-end: reference-point gradient from the offset gradients, one
 // wave per (b, q) of the nbq in the call.
 hipError_t launch_ref_grad(int dtype, const Params& p, uint64_t nbq, hipStream_t st);

@@ -1,0 +1,84 @@
+"""GPU parity of the binned owner backward (grad_value for calls with many
+samples per (batch, head, level): samples binned by band of value rows, each
+band summed in LDS and stored once, or added with atomics when its entries
+are split over several workgroups).
+
+The cases stress what the binning can get wrong: levels wider than a band
+(a sample's corners then span three bands), samples piled onto a few bands
+(split bands, atomic adds), corners outside the maps, an empty level, fp32
+accumulation, and the fused front-end -- each against the oracle.
+"""
+
+import pytest
+import torch
+
+from msda_cases import DTYPES, make_inputs
+from test_gpu_owner import BINNED, _analytic, check_grads, fwd_bwd, plan, reference_grads
+
+pytestmark = pytest.mark.gpu
+DEVICE = "cuda"
+
+BIN_CASES = [
+    # Q*K = 2400 per level: beyond the owner path's 2048.
+    dict(id="encoder_like", B=2, Q=600, M=4, D=32, K=4, shapes=[(24, 40), (12, 20), (6, 10)]),
+    # 300 px rows: wider than a 256-row band.
+    dict(id="wide_level", B=1, Q=800, M=2, D=32, K=4, shapes=[(6, 300), (3, 150)]),
+    # D = 64 and D = 16 heads (128- and 32-byte half rows).
+    dict(id="d64", B=1, Q=700, M=2, D=64, K=4, shapes=[(20, 30), (10, 15)]),
+    dict(id="d16", B=1, Q=700, M=4, D=16, K=4, shapes=[(30, 40), (15, 20)]),
+    # an empty level between two others
+    dict(id="empty_level", B=1, Q=700, M=2, D=32, K=4, shapes=[(20, 30), (0, 7), (5, 8)]),
+]
+
+
+def _inputs(case, dtype, **kw):
+    args = {k: v for k, v in case.items() if k != "id"}
+    return make_inputs(**args, dtype=dtype, device=DEVICE, **kw)
+
+
+@pytest.mark.parametrize("fp32_grad_accum", [False, True], ids=["native", "fp32acc"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("case", BIN_CASES, ids=[c["id"] for c in BIN_CASES])
+def test_binned_matches_reference(case, dtype, fp32_grad_accum):
+    value, shapes, starts, loc, attn = _inputs(case, dtype, loc_lo=-0.1, loc_hi=1.1)
+    if value.dtype == torch.float32 and case["D"] == 64:
+        pytest.skip("256-byte fp32 rows: not on the binned path")
+    assert plan(value, loc) == BINNED
+    print(f"binned {case['id']} {dtype} fp32acc={fp32_grad_accum}", flush=True)
+    g, grads = fwd_bwd(value, shapes, starts, loc, attn, fp32_grad_accum=fp32_grad_accum)
+    if case["id"] == "empty_level":  # grid_sample rejects empty maps: hand-derived float64
+        refs = [r.float() for r in _analytic(value, shapes, starts, loc, attn, g)]
+    else:
+        _, refs = reference_grads(value, shapes, loc, attn, g)
+    check_grads(grads, refs, dtype, shapes)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_binned_split_bands(dtype):
+    """Locations N(0.5, 0.01): each (b, m, level)'s 6000 samples land in one
+    or two bands, whose entries are split over several workgroups that add
+    their sums with atomics."""
+    B, Q, M, D, K = 1, 1500, 2, 32, 4
+    shapes = [(40, 60), (20, 30)]
+    value, sh, starts, loc, attn = make_inputs(B=B, Q=Q, M=M, D=D, shapes=shapes, K=K,
+                                               dtype=dtype, device=DEVICE)
+    gen = torch.Generator().manual_seed(5)
+    loc = (0.5 + 0.01 * torch.randn(loc.shape, generator=gen)).to(DEVICE, dtype)
+    assert plan(value, loc) == BINNED
+    g, grads = fwd_bwd(value, sh, starts, loc, attn)
+    _, refs = reference_grads(value, sh, loc, attn, g)
+    check_grads(grads, refs, dtype, sh)
+
+
+def test_binned_against_atomic_path(monkeypatch):
+    """Encoder-like call: the binned path and the row-dedup atomic path with
+    fp32 accumulation agree (same fp32 sums, another order)."""
+    case = BIN_CASES[0]
+    value, shapes, starts, loc, attn = _inputs(case, torch.float32)
+    g1, grads1 = fwd_bwd(value, shapes, starts, loc, attn)
+    monkeypatch.setenv("MSDA_BWD_BIN", "0")
+    g2, grads2 = fwd_bwd(value, shapes, starts, loc, attn, fp32_grad_accum=True)
+    assert torch.equal(g1, g2)
+    torch.testing.assert_close(grads1[0], grads2[0], rtol=1e-5, atol=1e-5)
+    for a, b in zip(grads1[1:], grads2[1:]):  # same dot products, other lane split
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)

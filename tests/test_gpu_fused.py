@@ -65,13 +65,15 @@ def test_fused_matches_float64_oracle(case, dtype, per_level):
     check(out, grads, ref_out, ref_grads, dtype)
 
 
-@pytest.mark.parametrize("priv", ["1", "0"], ids=["dedup", "direct"])
+@pytest.mark.parametrize("priv", ["1", "0", "bin"], ids=["dedup", "direct", "binned"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
 def test_fused_atomic_backward_kernels(dtype, priv, monkeypatch):
-    """The atomic backward kernels (row-dedup and direct) in their fused
-    variants; the default for these sizes is the owner-computes backward."""
+    """The other backward kernels (row-dedup and direct atomics, binned
+    owner) in their fused variants; the default for these sizes is the
+    owner-computes backward."""
     monkeypatch.setenv("MSDA_BWD_OWNER", "0")
-    monkeypatch.setenv("MSDA_BWD_PRIV", priv)
+    monkeypatch.setenv("MSDA_BWD_BIN", "1" if priv == "bin" else "0")
+    monkeypatch.setenv("MSDA_BWD_PRIV", "0" if priv == "0" else "1")
     case = FUSED_CASES[0]
     value, shapes, starts, ref, off, logits = make_fused_inputs(
         **kw(case), dtype=dtype, device=DEVICE, per_level=True)

@@ -31,7 +31,7 @@ def reference_grads(value, shapes, loc, attn, g):
 
 pytestmark = pytest.mark.gpu
 DEVICE = "cuda"
-OWNER, DEDUP = 2, 1
+OWNER, DEDUP, BINNED = 2, 1, 3
 DCODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 
@@ -65,15 +65,17 @@ def fwd_bwd(value, shapes, starts, loc, attn, seed=7, **kw):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
-@pytest.mark.parametrize("owner", ["1", "0"])
+@pytest.mark.parametrize("owner", ["1", "0", "bin"])
 def test_decoder_shapes_both_paths(dtype, owner, monkeypatch):
     """Decoder-style call (Q*K = 1200 per level, coarse levels split into
-    several bands) on the owner path and on the atomic one."""
-    monkeypatch.setenv("MSDA_BWD_OWNER", owner)
+    several bands) on the owner path, the atomic one and the binned one."""
+    monkeypatch.setenv("MSDA_BWD_OWNER", "1" if owner == "1" else "0")
+    monkeypatch.setenv("MSDA_BWD_BIN", "1" if owner == "bin" else "0")
     value, shapes, starts, loc, attn = make_inputs(
         B=2, Q=300, M=4, D=32, shapes=[(50, 84), (25, 42), (13, 21), (7, 11)], K=4,
         dtype=dtype, device=DEVICE, loc_lo=-0.1, loc_hi=1.1)
-    expect = OWNER if owner == "1" else DEDUP  # fp32: 38 KB of grad_out, the 40 KB build
+    # fp32: 38 KB of grad_out, the 40 KB build
+    expect = {"1": OWNER, "0": DEDUP, "bin": BINNED}[owner]
     assert plan(value, loc) == expect
     g, grads = fwd_bwd(value, shapes, starts, loc, attn)
     _, refs = reference_grads(value, shapes, loc, attn, g)
@@ -89,7 +91,7 @@ def test_grad_out_staging_builds(Q, dtype):
         B=1, Q=Q, M=2, D=32, shapes=[(30, 40), (15, 20), (8, 10)], K=2, dtype=dtype,
         device=DEVICE, loc_lo=-0.1, loc_hi=1.1)
     fits = Q * 32 * value.element_size() <= 40960
-    assert plan(value, loc) == (OWNER if fits else DEDUP)
+    assert (plan(value, loc) == OWNER) == fits  # beyond: the binned path
     g, grads = fwd_bwd(value, shapes, starts, loc, attn)
     _, refs = reference_grads(value, shapes, loc, attn, g)
     check_grads(grads, refs, dtype, shapes)
@@ -111,14 +113,14 @@ def test_row_widths(D, dtype):
     check_grads(grads, refs, dtype, shapes)
 
 
-@pytest.mark.parametrize("QK", [(128, 16), (128, 17)], ids=["QK2048_owner", "QK2176_atomic"])
+@pytest.mark.parametrize("QK", [(128, 16), (128, 17)], ids=["QK2048_owner", "QK2176_other"])
 def test_sample_count_boundary(QK):
     """Q*K = 2048 (8 samples per lane, the owner path's limit) and beyond."""
     Q, K = QK
     value, shapes, starts, loc, attn = make_inputs(
         B=1, Q=Q, M=2, D=32, shapes=[(20, 30), (10, 15)], K=K, dtype=torch.float32,
         device=DEVICE)
-    assert plan(value, loc) == (OWNER if Q * K <= 2048 else DEDUP)
+    assert (plan(value, loc) == OWNER) == (Q * K <= 2048)
     g, grads = fwd_bwd(value, shapes, starts, loc, attn)
     _, refs = reference_grads(value, shapes, loc, attn, g)
     check_grads(grads, refs, torch.float32, shapes)
@@ -214,6 +216,7 @@ def test_owner_and_atomic_paths_agree_on_decoder_preset(monkeypatch):
     assert plan(value, loc) == OWNER
     g1, grads1 = fwd_bwd(value, shapes, starts, loc, attn)
     monkeypatch.setenv("MSDA_BWD_OWNER", "0")
+    monkeypatch.setenv("MSDA_BWD_BIN", "0")
     g2, grads2 = fwd_bwd(value, shapes, starts, loc, attn, fp32_grad_accum=True)
     assert torch.equal(g1, g2)
     for a, b in zip(grads1[1:], grads2[1:]):  # other kernels: same sums, other order

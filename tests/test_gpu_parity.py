@@ -200,10 +200,13 @@ def test_backward_loc_and_attn_grads_are_deterministic():
 
 OVERRIDES = [
     dict(),                                          # defaults: owner backward
-    dict(MSDA_BWD_OWNER="0"),                        # atomic row-dedup backward
-    dict(MSDA_BWD_OWNER="0", MSDA_BWD_PRIV="0"),     # direct backward, 16 lanes/row
-    dict(MSDA_BWD_OWNER="0", MSDA_BWD_PRIV="0", MSDA_BWD_CB="16", MSDA_BWD_TS="4"),
-    dict(MSDA_BWD_OWNER="0", MSDA_BWD_PRIV="0", MSDA_BWD_CB="8", MSDA_BWD_TS="16"),
+    dict(MSDA_BWD_OWNER="0"),                        # binned owner backward (where it fits)
+    dict(MSDA_BWD_OWNER="0", MSDA_BWD_BIN="0"),      # atomic row-dedup backward
+    dict(MSDA_BWD_OWNER="0", MSDA_BWD_BIN="0", MSDA_BWD_PRIV="0"),  # direct, 16 lanes/row
+    dict(MSDA_BWD_OWNER="0", MSDA_BWD_BIN="0", MSDA_BWD_PRIV="0", MSDA_BWD_CB="16",
+         MSDA_BWD_TS="4"),
+    dict(MSDA_BWD_OWNER="0", MSDA_BWD_BIN="0", MSDA_BWD_PRIV="0", MSDA_BWD_CB="8",
+         MSDA_BWD_TS="16"),
     dict(MSDA_OWN_MIX="0"),                          # owner path, gradient workgroups last
     dict(MSDA_OWN_MIX="1"),                          # owner path, gradient workgroups first
     dict(MSDA_OWN_MIX="-1"),                         # owner path, gradient kernel launched apart

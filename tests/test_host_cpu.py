@@ -212,28 +212,44 @@ def test_custom_ops_are_registered_with_fake_shapes():
 
 def test_backward_plan(lib, monkeypatch):
     """Which grad_value path each preset's shapes take (host-only query)."""
-    owner, dedup, direct = 2, 1, 0
+    owner, dedup, direct, binned = 2, 1, 0, 3
     # decoder (B4 Q300 L4 K4, bf16): Q*K = 1200 per level, 64-byte rows
     assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 0) == owner
     assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 1) == owner  # deterministic
     assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 1) == dedup
     # encoder / Mask2Former: Q = S, far more samples per (b, m, level)
-    assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 0) == dedup
-    assert lib.msda_backward_plan(2, 21504, 8, 32, 21504, 3, 4, 0, 0) == dedup
+    assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 0) == binned
+    assert lib.msda_backward_plan(2, 21504, 8, 32, 21504, 3, 4, 0, 0) == binned
+    assert lib.msda_backward_plan(2, 21504, 8, 32, 21504, 3, 4, 2, 0) == binned
+    # binned path limits: head rows of 32, 64 or 128 bytes, D a power of two,
+    # bookkeeping within grad_attention_weights, <= 1024 (b, m, level) groups
+    assert lib.msda_backward_plan(2, 21504, 8, 64, 21504, 3, 4, 1, 0) == binned  # 128 B
+    assert lib.msda_backward_plan(2, 21504, 8, 64, 21504, 3, 4, 0, 0) != binned  # 256 B
+    assert lib.msda_backward_plan(2, 21504, 8, 24, 21504, 3, 4, 1, 0) == dedup   # D = 24
+    assert lib.msda_backward_plan(2, 21504, 8, 8, 21504, 3, 4, 1, 0) != binned   # 16 B
+    assert lib.msda_backward_plan(32, 21504, 8, 32, 21504, 4, 4, 1, 0) == binned  # 1024 groups
+    assert lib.msda_backward_plan(33, 21504, 8, 32, 21504, 4, 4, 1, 0) == dedup
+    assert lib.msda_backward_plan(1, 600, 2, 32, 1100, 2, 2, 1, 0) == binned  # 2200 B / group
+    assert lib.msda_backward_plan(1, 200000, 2, 32, 1100, 2, 2, 1, 0) == dedup  # bands > room
     # limits of the owner path: Q*K <= 2048, Q*D*elem <= 40960, rows of 16..256 bytes
     assert lib.msda_backward_plan(1, 600, 2, 32, 128, 2, 16, 1, 0) == owner  # Q*K = 2048
-    assert lib.msda_backward_plan(1, 600, 2, 32, 128, 2, 17, 1, 0) == dedup
+    assert lib.msda_backward_plan(1, 600, 2, 32, 128, 2, 17, 1, 0) != owner
     assert lib.msda_backward_plan(1, 600, 2, 32, 305, 2, 4, 1, 0) == owner   # 19520 B: 40 KB build
     assert lib.msda_backward_plan(1, 600, 2, 32, 640, 2, 2, 1, 0) == owner   # 40960 B
-    assert lib.msda_backward_plan(1, 600, 2, 32, 641, 2, 2, 1, 0) == dedup
+    assert lib.msda_backward_plan(1, 600, 2, 32, 641, 2, 2, 1, 0) != owner
     assert lib.msda_backward_plan(1, 600, 2, 32, 320, 2, 4, 0, 0) == owner   # 40960 B
-    assert lib.msda_backward_plan(1, 600, 2, 32, 321, 2, 4, 0, 0) == dedup
+    assert lib.msda_backward_plan(1, 600, 2, 32, 321, 2, 4, 0, 0) != owner
     assert lib.msda_backward_plan(1, 600, 2, 3, 100, 2, 4, 1, 0) == direct   # odd half row
     assert lib.msda_backward_plan(1, 600, 2, 128, 40, 2, 4, 1, 0) == owner   # 256-byte rows
     assert lib.msda_backward_plan(1, 600, 2, 256, 40, 2, 4, 1, 0) != owner
     # overrides read per call
     monkeypatch.setenv("MSDA_BWD_OWNER", "0")
+    # decoder: the bookkeeping (2404 B per group) exceeds grad_attention_weights (2400 B)
     assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 0) == dedup
+    assert lib.msda_backward_plan(4, 5600, 8, 32, 300, 4, 4, 2, 0) == binned
+    monkeypatch.setenv("MSDA_BWD_BIN", "0")
+    assert lib.msda_backward_plan(4, 5600, 8, 32, 300, 4, 4, 2, 0) == dedup
+    assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 0) == dedup
     monkeypatch.setenv("MSDA_BWD_PRIV", "0")
     assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 0) == direct
     # errors come back negated
