@@ -54,6 +54,8 @@ BACKWARD_KERNELS = {
     1: "msda_backward call (zero-fill + row-dedup atomic bwd_priv_kernel)",
     2: "msda_backward call (one owner_kernel launch: band workgroups for grad_value, then "
        "scatter-free gradient workgroups for grad_loc/grad_attn)",
+    3: "msda_backward call (zero-fill + binned owner: bin_kernel count/fill, bin_scan_kernel, "
+       "bin_acc_kernel for grad_value, then scatter-free bwd_kernel for grad_loc/grad_attn)",
 }
 
 
