@@ -237,6 +237,7 @@ __global__ __launch_bounds__(kBlock) void bin_scan_kernel(Params p, BinArgs a) {
   __shared__ uint32_t s_off[kBinMaxBands + 1];
   __shared__ uint32_t s_scan[kBlock];
   const int g = blockIdx.x;
+  if (g == 0 && threadIdx.x == 0) *a.next = 0u;
   const GroupLevel gl = group_level(p, a, g);
   if (gl.nk <= 0) {
     if (threadIdx.x == 0) a.nitems[g] = 0u;
@@ -290,9 +291,10 @@ __global__ __launch_bounds__(kBlock) void bin_scan_kernel(Params p, BinArgs a) {
       nch = (hi - lo + ceff - 1u) / ceff;
     }
     const uint32_t ex = block_excl_scan(nch, s_scan, total);
+    const uint32_t per = nch ? (hi - lo + nch - 1u) / nch : 0u;  // equal chunks
     for (uint32_t c = 0; c < nch; ++c) {
-      const uint32_t e0 = lo + c * ceff;
-      const uint32_t e1 = hi - e0 > ceff ? e0 + ceff : hi;
+      const uint32_t e0 = lo + c * per;
+      const uint32_t e1 = hi - e0 > per ? e0 + per : hi;
       const uint32_t idx = ibase + ex + c;
       if (idx < (uint32_t)a.cap)
         items[idx] = make_uint4((uint32_t)j | (nch > 1u ? 0x80000000u : 0u), e0, e1, 0u);
@@ -310,8 +312,8 @@ __global__ __launch_bounds__(kBlock) void bin_scan_kernel(Params p, BinArgs a) {
 // float atomics, no read-modify-write of LDS.  The sums leave through LDS so
 // that the stores (or atomics) cover whole rows.  RB = D * sizeof(T) bytes
 // of a grad_out row.  A: the element type of the target (T, or F32 for the fp32
-// scratch).  Persistent: workgroup w takes items w, w + grid, ... of the
-// flattened list, so every workgroup's loop ends.
+// scratch).  Persistent: workgroups take the items of the flattened list in
+// order from a global counter until it passes the item count.
 template <class T, class A, int RB, bool FUSED>
 __global__ __launch_bounds__(kBlock, 3) void bin_acc_kernel(Params p, BinArgs a) {
   constexpr int kD = RB / T::kBytes;  // channels
@@ -369,7 +371,15 @@ __global__ __launch_bounds__(kBlock, 3) void bin_acc_kernel(Params p, BinArgs a)
   const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.grad_out, p.gout_bytes);
   const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.grad_acc, p.acc_bytes);
 
-  for (uint32_t w = blockIdx.x; w < ntot; w += gridDim.x) {
+  __shared__ uint32_t s_w;
+  for (;;) {
+    // Next item from the global counter (every workgroup's loop ends once
+    // the counter passes the item count).
+    if (threadIdx.x == 0) s_w = atomicAdd(a.next, 1u);
+    __syncthreads();
+    const uint32_t w = s_w;
+    __syncthreads();
+    if (w >= ntot) break;
     int lo = 0, hi = a.ngroups;  // s_pre[lo] <= w < s_pre[hi]
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
@@ -661,7 +671,7 @@ bool bin_plan(int64_t B, int64_t Q, int64_t M, int64_t K, int64_t D, int64_t S, 
   if ((base & 3u) != 0) return false;
   const uint64_t avail = (uint64_t)(ng * qk * elem_bytes);
   const uint64_t n_cnt = (uint64_t)(ng * nbmax) * 4u;
-  uint64_t off_items = 2 * n_cnt + (uint64_t)ng * 4u;
+  uint64_t off_items = 2 * n_cnt + (uint64_t)ng * 4u + 4u;  // + the item counter
   off_items += (16u - ((base + off_items) & 15u)) & 15u;
   const uint64_t need = off_items + (uint64_t)(ng * cap) * 16u;
   if (need > avail || (uint64_t)(ng * qk * 2 * elem_bytes) > 0xffffffffull) return false;
@@ -670,6 +680,7 @@ bool bin_plan(int64_t B, int64_t Q, int64_t M, int64_t K, int64_t D, int64_t S, 
   a->counts = reinterpret_cast<uint32_t*>(ws);
   a->cursors = reinterpret_cast<uint32_t*>(ws + n_cnt);
   a->nitems = reinterpret_cast<uint32_t*>(ws + 2 * n_cnt);
+  a->next = reinterpret_cast<uint32_t*>(ws + 2 * n_cnt + (uint64_t)ng * 4u);
   a->items = reinterpret_cast<uint4*>(ws + off_items);
   a->ngroups = (int32_t)ng;
   a->nbmax = (int32_t)nbmax;

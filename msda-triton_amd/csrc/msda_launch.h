@@ -63,12 +63,13 @@ hipError_t launch_owner(int dtype, bool fused, const Params& p, const Params& pd
 constexpr int kBinAccFloats = 8192;  // fp32 band accumulator: P * D floats (32 KB)
 constexpr int kBinMaxBands = 4096;   // bands per level
 constexpr int kBinMaxGroups = 1024;  // (b, m, level) groups per launch
-constexpr int kBinChunk = 2048;      // entries per work item (at least)
+constexpr int kBinChunk = 4096;      // entries per work item (at most, unless items run short)
 struct BinArgs {
   uint32_t* entries;  // [group][Q*K] sample ids q*K + k, by band (in grad_loc)
   uint32_t* counts;   // [group][nbmax] samples keyed to each key (2^log2k pixels)
   uint32_t* cursors;  // [group][nbmax] first entry of each key, then fill cursor
   uint32_t* nitems;   // [group] work items
+  uint32_t* next;     // work-item counter of bin_acc_kernel (zeroed by bin_scan_kernel)
   uint4* items;       // [group][cap] (band | split << 31, first entry, end entry, 0)
   uint32_t loc_bytes, attn_bytes;
   int32_t ngroups, nbmax, cap, nqb, log2p, log2k, chunk;  // bands of 2^log2p pixels
