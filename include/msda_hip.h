@@ -85,7 +85,7 @@ int msda_forward(const void* value, const int64_t* spatial_shapes,
  *                           accumulated in place with the dtype's own atomics
  *                           (fp32 add, packed fp16/bf16 add).  Non-NULL: an
  *                           fp32 scratch array of B*S*M*D floats; the atomic
- *                           paths accumulate there with fp32 atomics and
+ *                           and binned paths accumulate there in fp32 and
  *                           round once into grad_value.  This is the
  *                           reference's `fp32_grad_accum=True`
  *                           (src/msda_triton/ops.py:76-77,91-92).  For
