@@ -291,10 +291,13 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
   } else if (compute) {
     // The owner paths run the direct kernel without its scatter: no atomics
     // to spread over pairs, so it takes the forward's launch shape.
+    // Binned path: 4 sample slots per pair by default (measured faster than
+    // the forward's 1 for the encoder / pixel-decoder grids it serves).
     const bool no_scatter = owner || binned;
+    const int ts_pref = !no_scatter ? bwd_ts_pref()
+                        : binned && fwd_ts_pref() <= 0 ? 4 : fwd_ts_pref();
     Shape sh;
-    if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, !no_scatter,
-                      no_scatter ? fwd_ts_pref() : bwd_ts_pref(),
+    if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, !no_scatter, ts_pref,
                       no_scatter ? fwd_cb_pref() : bwd_cb_pref(), &sh))
       return MSDA_ERR_UNSUPPORTED_SHAPE;
     const int64_t bs = slice_batch(d);
