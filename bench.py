@@ -30,6 +30,9 @@ Prints ONE JSON line:
                (value / offset+logit / output) on the library's MFMA kernels vs
                torch's linear (+ masked_fill) and its backward
   cpu_baseline the CPU oracle (grid_sample restatement) on the host cores
+  rel_err      the timed steps' output and three gradients against that
+               oracle run (norm-relative; max-abs in cpu_baseline)
+  peak_mb      peak device memory of one fwd+bwd through the public operator
 """
 
 from __future__ import annotations
@@ -85,10 +88,35 @@ def _traffic(preset: str, kernel: str):
     return None
 
 
-def cpu_baseline(preset: str, max_seconds: float = 25.0) -> dict:
+def _cgroup_cpus():
+    """CPUs the cgroup's CFS quota grants (cpu.max), or None without a quota."""
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        return None if quota == "max" else round(int(quota) / int(period), 2)
+    except (OSError, ValueError):
+        return None
+
+
+def accuracy(got, ref) -> dict:
+    """Norm-relative and max-abs error of the GPU results against the oracle
+    (the reference's benchmark reports max_err against its fp32 reference,
+    benchmarks/modal_benchmark.py:283-287)."""
+    res = {}
+    for name, x, r in zip(("out", "grad_value", "grad_loc", "grad_attn"), got, ref):
+        x = x.detach().double().cpu().reshape(r.shape)
+        r = r.double()
+        den = r.norm().item()
+        res[name] = {"rel_err": float(f"{(x - r).norm().item() / (den or 1.0):.3e}"),
+                     "max_abs_err": float(f"{(x - r).abs().max().item():.3e}")}
+    return res
+
+
+def cpu_baseline(preset: str, max_seconds: float = 25.0, gpu_results=None) -> dict:
     """The oracle (msda_reference restatement: per-level F.grid_sample + torch
     autograd) on fp32 upcasts of the same inputs, fwd+bwd, on this host's
-    cores: 1 warm-up, then the median of up to 5 runs within ~max_seconds."""
+    cores: 1 warm-up, then the median of up to 5 runs within ~max_seconds.
+    `gpu_results` (out, grad_value, grad_loc, grad_attn of the timed GPU
+    steps, same inputs and grad_out) are compared with the oracle's."""
     import torch
 
     from msda_triton_amd import presets
@@ -96,11 +124,12 @@ def cpu_baseline(preset: str, max_seconds: float = 25.0) -> dict:
     sys.path.insert(0, str(ROOT))
     from oracle import run_reference_fp32
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    affinity = len(os.sched_getaffinity(0))
+    threads = affinity
     torch.set_num_threads(threads)
     value, shapes, _, loc, attn = presets.make_preset_inputs(preset, device="cpu")
     g = presets.make_grad_out(preset, device="cpu")
-    run_reference_fp32(value, shapes, loc, attn, g)  # warm-up
+    ref_out, ref_grads = run_reference_fp32(value, shapes, loc, attn, g)  # warm-up
     times = []
     t_start = time.perf_counter()
     while len(times) < 5 and (time.perf_counter() - t_start) < max_seconds:
@@ -109,7 +138,7 @@ def cpu_baseline(preset: str, max_seconds: float = 25.0) -> dict:
         times.append(time.perf_counter() - t0)
     fwd_b, bwd_b = presets.algorithmic_bytes(preset)
     t = statistics.median(times)
-    return {
+    res = {
         "value": round((fwd_b + bwd_b) / t / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
@@ -117,7 +146,12 @@ def cpu_baseline(preset: str, max_seconds: float = 25.0) -> dict:
         "sample": f"{preset} preset, full batch, fwd+bwd of the grid_sample oracle in fp32 "
                   f"(median of {len(times)} runs, {t * 1e3:.1f} ms each) on {_cpu_model()}",
         "ms_per_step": round(t * 1e3, 3),
+        "affinity_cpus": affinity,
+        "cgroup_cpu_quota": _cgroup_cpus(),
     }
+    if gpu_results is not None:
+        res["gpu_vs_oracle"] = accuracy(gpu_results, (ref_out,) + tuple(ref_grads))
+    return res
 
 
 def _capture(fn, reps, dev):
@@ -545,18 +579,21 @@ def main() -> int:
     bwd_det_us = per_call_us(deterministic_backward(lib, value, shapes, starts, loc, attn,
                                                     grad_out), reps=10, replays=5)
 
-    # Cold variants: a 512 MiB write before every call evicts L2 and the
-    # 256 MiB Infinity Cache, so the inputs come from HBM; the flush's own
-    # time (measured alone) is subtracted.
-    flush_buf = torch.empty(128 << 20, dtype=torch.float32, device=dev)
+    # Cold variants: a 512 MiB read before every call evicts L2 and the
+    # 256 MiB Infinity Cache, so the inputs come from HBM; the flush only
+    # reads (row maxima: 512 KiB written), so it leaves no dirty lines to be
+    # written back during the timed call.  The flush's own time (measured
+    # alone) is subtracted.
+    flush_buf = torch.ones(128 << 20, dtype=torch.float32, device=dev).view(-1, 4096)
+    flush_max = torch.empty(flush_buf.shape[0], dtype=torch.float32, device=dev)
 
     def flush():
-        flush_buf.zero_()
+        torch.amax(flush_buf, dim=1, out=flush_max)
 
     flush_us = per_call_us(flush, reps=10, replays=5)
     fwd_cold_us = per_call_us(lambda: (flush(), fwd()), reps=10, replays=5) - flush_us
     bwd_cold_us = per_call_us(lambda: (flush(), bwd()), reps=10, replays=5) - flush_us
-    del flush_buf
+    del flush_buf, flush_max
 
     # Through the public autograd operator, eagerly (host launch cost included).
     from msda_triton_amd import multi_scale_deformable_attention as msda
@@ -574,6 +611,16 @@ def main() -> int:
     for _ in range(5):
         api_step()
     torch.cuda.synchronize()
+    # Peak device memory of one fwd+bwd through the public operator (the
+    # reference's peak_mb, benchmarks/modal_benchmark.py:180-190): inputs,
+    # output, gradients and any scratch the call allocates.
+    v_l.grad = l_l.grad = a_l.grad = None
+    torch.cuda.synchronize()
+    base_mb = torch.cuda.memory_allocated() / 2 ** 20
+    torch.cuda.reset_peak_memory_stats()
+    api_step()
+    torch.cuda.synchronize()
+    peak_mb = torch.cuda.max_memory_allocated() / 2 ** 20
     n_api = 50
     t0 = time.perf_counter()
     for _ in range(n_api):
@@ -621,6 +668,8 @@ def main() -> int:
         "fwd_cold_us": round(fwd_cold_us, 3),
         "bwd_cold_us": round(bwd_cold_us, 3),
         "api_eager_fwd_bwd_us": round(api_us, 1),
+        "peak_mb": round(peak_mb, 1),
+        "peak_mb_above_resident": round(peak_mb - base_mb, 1),
         "roofline": {
             "bound": "hbm",
             "achieved": round(bwd_gbps, 1),
@@ -652,7 +701,12 @@ def main() -> int:
         record["fused_front_end"] = fused_front_end_times(lib)
         record["projections"] = projection_times(lib)
     if not args.no_cpu_baseline:
-        record["cpu_baseline"] = cpu_baseline(args.preset)
+        # The timed steps' results (the last step's; every step computes the
+        # same) against the oracle on the same inputs.
+        record["cpu_baseline"] = cpu_baseline(
+            args.preset, gpu_results=(out, grad_value, grad_loc, grad_attn))
+        record["rel_err"] = {k: v["rel_err"]
+                             for k, v in record["cpu_baseline"]["gpu_vs_oracle"].items()}
     print(json.dumps(record), flush=True)
     return 0
 

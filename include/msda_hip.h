@@ -305,6 +305,33 @@ int msda_backward_plan(int64_t batch, int64_t num_keys, int64_t num_heads, int64
                        int64_t num_queries, int64_t num_levels, int64_t num_points, int dtype,
                        int deterministic);
 
+/*
+ * Launch-shape and path overrides, for sweeps and for tests that run every
+ * kernel variant.  No counterpart in the reference, which picks its launch
+ * configuration by Triton autotuning (src/msda_triton/kernels.py:54-65).
+ * By default no knob is set and every call makes the automatic choice; the
+ * library reads no environment variable.  The table is process-wide (every
+ * device, every thread): set it before the calls it should affect.
+ *   knob    one of the MSDA_KNOB_* codes below
+ *   value   the knob's value, or MSDA_OVERRIDE_AUTO to restore the
+ *           automatic choice
+ * Returns MSDA_OK, or MSDA_ERR_INVALID_ARGUMENT for an unknown knob.
+ */
+#define MSDA_KNOB_FWD_TS 0      /* forward / scatter-free gradient: sample slots per pair */
+#define MSDA_KNOB_FWD_CB 1      /* ... bytes per lane load, at most (16, 8, 4, 2) */
+#define MSDA_KNOB_BWD_TS 2      /* atomic backward: sample slots per pair */
+#define MSDA_KNOB_BWD_CB 3      /* atomic backward: bytes per lane load, at most */
+#define MSDA_KNOB_BWD_PRIV 4    /* 0: direct atomic kernel instead of the row-dedup one */
+#define MSDA_KNOB_BWD_OWNER 5   /* 0: no owner-computes backward */
+#define MSDA_KNOB_BWD_BIN 6     /* 0: no binned backward */
+#define MSDA_KNOB_OWN_MIX 7     /* owner launch order: 2 auto, 0 gradient workgroups last,
+                                   1 first, -1 a launch of their own */
+#define MSDA_KNOB_OWN_ROWS 8    /* owner path: rows per band, at most (64..2048) */
+#define MSDA_KNOB_OWN_ENTRIES 9 /* owner path: corner entries per band the level split aims at */
+#define MSDA_NUM_KNOBS 10
+#define MSDA_OVERRIDE_AUTO (-2147483647 - 1)
+int msda_set_launch_override(int knob, int value);
+
 #ifdef __cplusplus
 }
 #endif

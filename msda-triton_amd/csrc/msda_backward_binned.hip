@@ -23,9 +23,10 @@
 //   bin_kernel<fill>   writes each sample's id (q * K + k) at its band's
 //                      cursor (LDS ranks + one global add per band);
 //   bin_acc_kernel     per work item: the entries' corner contributions to
-//                      the band's rows are summed in LDS (fp32 ds_add), then
+//                      the band's rows are summed in fp32 registers, then
 //                      the band is stored (its only item) or added with
-//                      buffer atomics (items of a band split in chunks).
+//                      buffer atomics (items of a band split in chunks, or
+//                      any band when the level table lets levels share rows).
 // No workspace: the entry lists live in grad_sampling_locations (4 bytes per
 // sample, its size at least) and the counts, cursors and items in
 // grad_attention_weights, both written in full afterwards by the gradient
@@ -281,6 +282,20 @@ __global__ __launch_bounds__(kBlock) void bin_scan_kernel(Params p, BinArgs a) {
   uint32_t ceff = (vtot + room - 1u) / room;
   if (ceff < (uint32_t)a.chunk) ceff = (uint32_t)a.chunk;
 
+  // A band is stored with plain stores only when it is one item and its
+  // rows belong to its level alone: the level table must be the cumulative
+  // one (start_l = sum of the H W before it, covering S), as
+  // level_start_index = None gives.  Levels of any other table may share
+  // rows, so every band then adds into the zeroed accumulator with atomics.
+  bool shared = false;
+  {
+    int64_t acc = 0;
+    for (int l = 0; l < p.L; ++l) {
+      if (p.starts[l] != acc) shared = true;
+      acc += p.shapes[2 * l] * p.shapes[2 * l + 1];
+    }
+    if (acc != (int64_t)p.S) shared = true;
+  }
   uint4* items = a.items + (uint32_t)g * a.cap;
   uint32_t ibase = 0u;
   for (int j0 = 0; j0 < gl.nb; j0 += kBlock) {
@@ -297,7 +312,7 @@ __global__ __launch_bounds__(kBlock) void bin_scan_kernel(Params p, BinArgs a) {
       const uint32_t e1 = hi - e0 > per ? e0 + per : hi;
       const uint32_t idx = ibase + ex + c;
       if (idx < (uint32_t)a.cap)
-        items[idx] = make_uint4((uint32_t)j | (nch > 1u ? 0x80000000u : 0u), e0, e1, 0u);
+        items[idx] = make_uint4((uint32_t)j | (nch > 1u || shared ? 0x80000000u : 0u), e0, e1, 0u);
     }
     ibase += total;
   }

@@ -22,9 +22,12 @@
 //
 // The sums are the reference's, accumulated in fp32 and rounded once, in
 // every mode (the fp32_grad_accum choice is moot here).  Their order within a
-// row follows the CSR fill, so grad_value is not bitwise reproducible across
-// runs (like the reference's atomics); grad_loc / grad_attn come from the
-// direct backward kernel launched without its scatter.
+// row follows the CSR, whose order is fixed by the inputs (each wave counts
+// into its own row counters, so an entry's rank depends only on that wave's
+// instructions in program order): grad_value is bitwise reproducible across
+// runs, unlike the reference's atomics, and the deterministic entry points
+// use this path unchanged.  grad_loc / grad_attn come from the direct
+// backward kernel's body without its scatter.
 //
 // Bands: for a standard level table (start_0 = 0, start_{l+1} = start_l +
 // H_l W_l, levels covering [0, S): what level_start_index = None gives) each
@@ -35,11 +38,10 @@
 // (handled one level per round: the first round stores every row, later
 // rounds add into the rows they touch -- the workgroup is their only
 // writer) or none (rows stored as zeros).
-#include <stdlib.h>
-
 #include <algorithm>
 #include <atomic>
 
+#include "../../include/msda_hip.h"
 #include "msda_bwd_body.h"
 #include "msda_launch.h"
 
@@ -675,13 +677,11 @@ hipError_t launch_t(const Params& p, const Params& pd, hipStream_t st) {
 
 }  // namespace
 
-// Band geometry overrides for sweeps (read per call): MSDA_OWN_ROWS, the
-// most rows per band (64..kOwnRows), and MSDA_OWN_ENTRIES, the corner
-// entries per band the level split aims at (>= 64).
-static int64_t own_env(const char* name, int64_t dflt, int64_t lo, int64_t hi) {
-  const char* v = getenv(name);
-  if (!v) return dflt;
-  const int64_t x = atoll(v);
+// Band geometry overrides for sweeps: MSDA_KNOB_OWN_ROWS, the most rows per
+// band (64..kOwnRows), and MSDA_KNOB_OWN_ENTRIES, the corner entries per
+// band the level split aims at (>= 64).
+static int64_t own_knob(int knob, int64_t dflt, int64_t lo, int64_t hi) {
+  const int64_t x = launch_override(knob, (int)dflt);
   return x < lo ? lo : x > hi ? hi : x;
 }
 
@@ -723,12 +723,12 @@ bool owner_plan(int64_t B, int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L
   // 42.5), else half that (small grids: a band's own time is the kernel's).
   const int64_t ent = 4 * Q * K;
   const int64_t want = own_slots(big ? 2 : 4) * 4 / 5;
-  const bool env_split = getenv("MSDA_OWN_ENTRIES") != nullptr;
+  const bool env_split = launch_override_set(MSDA_KNOB_OWN_ENTRIES);
   auto plan_split = [&](int64_t rows, bool* full) {
     const int64_t fine = (S + rows - 1) / rows;
     auto wgs = [&](int64_t s) { return B * p->M * (std::max(fine, s) + (L - 1) * s); };
     if (env_split) {
-      const int64_t target = own_env("MSDA_OWN_ENTRIES", kOwnBandFill, 64, 1 << 20);
+      const int64_t target = own_knob(MSDA_KNOB_OWN_ENTRIES, kOwnBandFill, 64, 1 << 20);
       *full = true;
       return (ent + target - 1) / target;
     }
@@ -740,10 +740,10 @@ bool owner_plan(int64_t B, int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L
     *full = wgs(s) >= want;
     return s;
   };
-  int64_t rows = own_env("MSDA_OWN_ROWS", kOwnRows, 64, kOwnRows);
+  int64_t rows = own_knob(MSDA_KNOB_OWN_ROWS, kOwnRows, 64, kOwnRows);
   bool full = true;
   int64_t split = plan_split(rows, &full);
-  if (!full && !getenv("MSDA_OWN_ROWS")) {
+  if (!full && !launch_override_set(MSDA_KNOB_OWN_ROWS)) {
     rows = kOwnRows / 2;
     split = plan_split(rows, &full);
   }

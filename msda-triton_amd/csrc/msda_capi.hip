@@ -1,7 +1,7 @@
 // C ABI of the MSDA operator: argument checks, batch slicing and launch-shape
 // selection around the kernels in msda_forward.hip / msda_backward.hip.
 // Declarations and the contract live in include/msda_hip.h.
-#include <stdlib.h>
+#include <atomic>
 
 #include "../../include/msda_hip.h"
 #include "msda_launch.h"
@@ -78,30 +78,32 @@ void finish_params(const Shape& s, int max_records, Params* p) {
   p->ts_rt = s.ts;
 }
 
-static int env_int(const char* name) {
-  const char* v = getenv(name);
-  return v ? atoi(v) : 0;
+// Override table: 0 = automatic, else (value << 1) | 1.  Process-wide, set
+// only through msda_set_launch_override; relaxed atomics, so a call racing
+// a change sees either value of each knob.
+static std::atomic<int64_t> g_override[kNumKnobs];
+
+int launch_override(int knob, int dflt) {
+  const int64_t v = g_override[knob].load(std::memory_order_relaxed);
+  return (v & 1) ? (int)(v >> 1) : dflt;
 }
 
-// Launch-shape overrides (sweeps and tests), read on every call: slots per
-// pair (power of two), upper bound on the bytes per lane load (16, 8, 4, 2),
-// and MSDA_BWD_PRIV=0 to use the direct backward instead of the row-dedup
-// one.  getenv costs well under a microsecond next to the launch.
-static int fwd_ts_pref() { return env_int("MSDA_FWD_TS"); }
-static int bwd_ts_pref() { return env_int("MSDA_BWD_TS"); }
-static int fwd_cb_pref() { return env_int("MSDA_FWD_CB"); }
-static int bwd_cb_pref() { return env_int("MSDA_BWD_CB"); }
-static bool bwd_priv_enabled() {
-  return getenv("MSDA_BWD_PRIV") == nullptr || env_int("MSDA_BWD_PRIV") != 0;
+bool launch_override_set(int knob) {
+  return (g_override[knob].load(std::memory_order_relaxed) & 1) != 0;
 }
-// MSDA_BWD_OWNER=0: atomic backward even where the owner-computes one applies.
-static bool bwd_owner_enabled() {
-  return getenv("MSDA_BWD_OWNER") == nullptr || env_int("MSDA_BWD_OWNER") != 0;
-}
-// MSDA_BWD_BIN=0: no binned owner path (the atomic kernels instead).
-static bool bwd_bin_enabled() {
-  return getenv("MSDA_BWD_BIN") == nullptr || env_int("MSDA_BWD_BIN") != 0;
-}
+
+// Slots per pair (power of two), upper bound on the bytes per lane load (16,
+// 8, 4, 2; 0 = automatic), and the backward path switches (0 = off).
+static int fwd_ts_pref() { return launch_override(MSDA_KNOB_FWD_TS, 0); }
+static int bwd_ts_pref() { return launch_override(MSDA_KNOB_BWD_TS, 0); }
+static int fwd_cb_pref() { return launch_override(MSDA_KNOB_FWD_CB, 0); }
+static int bwd_cb_pref() { return launch_override(MSDA_KNOB_BWD_CB, 0); }
+// Off: the direct backward instead of the row-dedup one.
+static bool bwd_priv_enabled() { return launch_override(MSDA_KNOB_BWD_PRIV, 1) != 0; }
+// Off: atomic (or binned) backward even where the owner-computes one applies.
+static bool bwd_owner_enabled() { return launch_override(MSDA_KNOB_BWD_OWNER, 1) != 0; }
+// Off: no binned owner path (the atomic kernels instead).
+static bool bwd_bin_enabled() { return launch_override(MSDA_KNOB_BWD_BIN, 1) != 0; }
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 static int elem_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
@@ -137,6 +139,36 @@ static int64_t slice_batch(const Dims& d) {
 
 static int status(hipError_t e) { return e == hipSuccess ? MSDA_OK : MSDA_ERR_LAUNCH; }
 
+static const char* at(const void* base, int64_t elems, int e) {
+  return static_cast<const char*>(base) + elems * e;
+}
+static char* at(void* base, int64_t elems, int e) { return static_cast<char*>(base) + elems * e; }
+
+// Binned owner path: batch slices of at most kBinMaxGroups (b, m, level)
+// groups, each within the 32-bit slice limits, whose grad_loc / grad_attn
+// hold the slice's bookkeeping (bin_plan).  On success *bs_out is the slice
+// size.  grad_loc == NULL (msda_backward_plan): buffers at 256-byte aligned
+// addresses are assumed, so the alignment padding is the one a torch
+// allocation would see.
+static bool binned_slices(const Dims& d, int e, void* grad_loc, void* grad_attn,
+                          int64_t* bs_out) {
+  const int64_t per_b = d.M * d.L;
+  int64_t bs = slice_batch(d);
+  if (per_b <= 0 || per_b > kBinMaxGroups || bs <= 0) return false;
+  if (bs > kBinMaxGroups / per_b) bs = kBinMaxGroups / per_b;
+  for (int64_t b0 = 0; b0 < d.B; b0 += bs) {
+    const int64_t nb = d.B - b0 < bs ? d.B - b0 : bs;
+    const int64_t so = b0 * d.Q * d.M * d.L * d.K;
+    void* gl = grad_loc ? at(grad_loc, so * 2, e)
+                        : reinterpret_cast<void*>((uintptr_t)(so * 2 * e));
+    void* ga = grad_attn ? at(grad_attn, so, e) : reinterpret_cast<void*>((uintptr_t)(so * e));
+    BinArgs ba;
+    if (!bin_plan(nb, d.Q, d.M, d.K, d.D, d.S, d.L, e, gl, ga, &ba)) return false;
+  }
+  *bs_out = bs;
+  return true;
+}
+
 static void base_params(const Dims& d, int64_t b0, int64_t bs, int dtype, Params* p) {
   const int e = elem_bytes(dtype);
   p->S = (int32_t)d.S;
@@ -155,11 +187,6 @@ static void base_params(const Dims& d, int64_t b0, int64_t bs, int dtype, Params
   p->div_k = make_fastdiv((uint32_t)(d.K > 0 ? d.K : 1));
   (void)b0;
 }
-
-static const char* at(const void* base, int64_t elems, int e) {
-  return static_cast<const char*>(base) + elems * e;
-}
-static char* at(void* base, int64_t elems, int e) { return static_cast<char*>(base) + elems * e; }
 
 // Fused front-end arguments (NULL when the call takes locations + weights).
 struct FusedArgs {
@@ -253,18 +280,9 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
       !owner && !det && grad_value_accum != nullptr && dtype != kF32 && n_val > 0;
   // Binned owner path (many samples per (b, m, level)): every slice's
   // grad_loc / grad_attn must hold its bookkeeping (bin_plan).
-  bool binned = false;
-  if (compute && !owner && !deterministic && bwd_bin_enabled()) {
-    const int64_t bs0 = slice_batch(d);
-    binned = bs0 > 0;
-    for (int64_t b0 = 0; binned && b0 < d.B; b0 += bs0) {
-      const int64_t nb = d.B - b0 < bs0 ? d.B - b0 : bs0;
-      const int64_t so = b0 * d.Q * d.M * d.L * d.K;
-      BinArgs ba;
-      binned = bin_plan(nb, d.Q, d.M, d.K, d.D, d.S, d.L, e, at(grad_loc, so * 2, e),
-                        at(grad_attn, so, e), &ba);
-    }
-  }
+  int64_t bs_bin = 0;
+  const bool binned = compute && !owner && !deterministic && bwd_bin_enabled() &&
+                      binned_slices(d, e, grad_loc, grad_attn, &bs_bin);
   const AccMode mode = det ? kAccI64 : fp32_acc ? kAccF32 : kAccNative;
   void* acc = det ? det_workspace : fp32_acc ? static_cast<void*>(grad_value_accum) : grad_value;
   const int acc_e = det ? 8 : fp32_acc ? 4 : e;
@@ -300,7 +318,7 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
     if (!choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, !no_scatter, ts_pref,
                       no_scatter ? fwd_cb_pref() : bwd_cb_pref(), &sh))
       return MSDA_ERR_UNSUPPORTED_SHAPE;
-    const int64_t bs = slice_batch(d);
+    const int64_t bs = binned ? bs_bin : slice_batch(d);
     if (bs <= 0) return MSDA_ERR_UNSUPPORTED_SHAPE;
     const int64_t ref_per_b = d.Q * (f && f->ref_levels ? d.L : 1) * 2;
     // Fused, owner path: the gradient workgroups also form grad_ref when
@@ -365,10 +383,8 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
         po.own_est = own.own_est;
         po.own_big = own.own_big;
         po.div_g = make_fastdiv((uint32_t)own.g_real);
-        {  // sweeps: MSDA_OWN_MIX=0 gradient workgroups last, 1 first, -1 two launches
-          const char* mx = getenv("MSDA_OWN_MIX");
-          po.own_mix = mx ? atoi(mx) : 2;
-        }
+        // Sweeps: 0 gradient workgroups last, 1 first, -1 a launch of their own.
+        po.own_mix = launch_override(MSDA_KNOB_OWN_MIX, 2);
         if (f) po.ref_bytes = (uint32_t)(nb * ref_per_b * e);
         finish_params(sh, kBwdRecords, &p);
         // The owner launch carries the grad_loc / grad_attn workgroups when
@@ -713,7 +729,16 @@ extern "C" const char* msda_error_string(int code) {
   }
 }
 
-extern "C" int msda_abi_version(void) { return (1 << 16) | 4; }
+extern "C" int msda_abi_version(void) { return (1 << 16) | 5; }
+
+static_assert(MSDA_NUM_KNOBS == kNumKnobs, "knob table");
+
+extern "C" int msda_set_launch_override(int knob, int value) {
+  if (knob < 0 || knob >= kNumKnobs) return MSDA_ERR_INVALID_ARGUMENT;
+  const int64_t v = value == MSDA_OVERRIDE_AUTO ? 0 : ((int64_t)value * 2) | 1;
+  g_override[knob].store(v, std::memory_order_relaxed);
+  return MSDA_OK;
+}
 
 extern "C" int msda_backward_plan(int64_t batch, int64_t num_keys, int64_t num_heads,
                                   int64_t head_dim, int64_t num_queries, int64_t num_levels,
@@ -727,10 +752,9 @@ extern "C" int msda_backward_plan(int64_t batch, int64_t num_keys, int64_t num_h
   base_params(d, 0, d.B, dtype, &own);
   if (compute && bwd_owner_enabled() && owner_plan(d.B, d.Q, d.K, d.D, d.S, d.L, e, &own))
     return MSDA_BACKWARD_OWNER;
-  const int64_t bs = slice_batch(d);
-  BinArgs ba;
-  if (compute && !deterministic && bwd_bin_enabled() && bs > 0 &&
-      bin_plan(bs < d.B ? bs : d.B, d.Q, d.M, d.K, d.D, d.S, d.L, e, nullptr, nullptr, &ba))
+  int64_t bs_bin = 0;
+  if (compute && !deterministic && bwd_bin_enabled() &&
+      binned_slices(d, e, nullptr, nullptr, &bs_bin))
     return MSDA_BACKWARD_BINNED;
   Shape sh;
   if (compute && !choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, true,

@@ -20,6 +20,14 @@ struct Shape {
 
 FastDiv make_fastdiv(uint32_t d);
 
+// Launch-shape and path overrides (msda_set_launch_override; sweeps and the
+// tests that run every kernel variant).  Knob ids are the MSDA_KNOB_* codes
+// of the header.  A call that nobody has overridden reads one relaxed atomic
+// per knob it consults and gets `dflt`.
+constexpr int kNumKnobs = 10;
+int launch_override(int knob, int dflt);
+bool launch_override_set(int knob);
+
 // Picks CB/G for a row of `row_bytes` and the slot count TS for LK samples
 // over `npairs` (b, q, m) pairs; *_pref > 0 override the choice (sweeps).
 // Returns false if the row is too wide for one wave.

@@ -9,6 +9,7 @@ computation goes through this library or raises.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -41,7 +42,15 @@ SIGNATURES = {
     "msda_error_string": (ctypes.c_char_p, [_INT]),
     "msda_abi_version": (_INT, []),
     "msda_backward_plan": (_INT, [_I64] * 7 + [_INT, _INT]),
+    "msda_set_launch_override": (_INT, [_INT, _INT]),
 }
+
+# msda_set_launch_override knobs (MSDA_KNOB_* in the header).
+KNOBS = {
+    "FWD_TS": 0, "FWD_CB": 1, "BWD_TS": 2, "BWD_CB": 3, "BWD_PRIV": 4, "BWD_OWNER": 5,
+    "BWD_BIN": 6, "OWN_MIX": 7, "OWN_ROWS": 8, "OWN_ENTRIES": 9,
+}
+OVERRIDE_AUTO = -(2 ** 31)
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -73,6 +82,24 @@ def load() -> ctypes.CDLL:
                 fn.argtypes = args
             _lib = lib
     return _lib
+
+
+@contextlib.contextmanager
+def launch_overrides(**knobs: int):
+    """Set launch-shape / path overrides (``BWD_OWNER=0``, ``FWD_TS=4``, ...)
+    for the calls inside the block; every knob named is reset to the
+    automatic choice on exit.  Process-wide: for sweeps and tests."""
+    lib = load()
+    codes = []
+    try:
+        for name, value in knobs.items():
+            code = KNOBS[name]
+            codes.append(code)
+            check(lib.msda_set_launch_override(code, int(value)), "msda_set_launch_override")
+        yield
+    finally:
+        for code in codes:
+            lib.msda_set_launch_override(code, OVERRIDE_AUTO)
 
 
 def check(rc: int, what: str) -> None:

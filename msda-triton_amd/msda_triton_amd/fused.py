@@ -26,7 +26,8 @@ from torch.autograd.function import once_differentiable
 
 from . import _native
 from .ops import (_DTYPE_CODE, _FLOAT_DTYPES, _as_index_tensor, _on_device, _ptr, _stream,
-                  _use_deterministic, _use_fp32_grad_accum, deterministic_workspace)
+                  _use_deterministic, _use_fp32_grad_accum, aligned_rows,
+                  deterministic_workspace)
 
 
 def fused_forward_raw(value, spatial_shapes, level_start_index, reference_points,
@@ -56,7 +57,7 @@ def fused_backward_raw(value, spatial_shapes, level_start_index, reference_point
     ``(grad_value, grad_reference_points or None, grad_offsets, grad_logits)``."""
     B, S, M, D = value.shape
     _, Q, _, L, K, _ = sampling_offsets.shape
-    grad_out = grad_out.reshape(B, Q, M, D).contiguous()
+    grad_out = aligned_rows(grad_out.reshape(B, Q, M, D))
     grad_value = torch.empty_like(value)  # written in full by the library
     grad_ref = torch.empty_like(reference_points) if need_ref_grad else None
     grad_off = torch.empty_like(sampling_offsets)

@@ -138,13 +138,23 @@ class _MSDAFunction(torch.autograd.Function):
         return grad_value, None, None, grad_loc, grad_attn, None, None
 
 
+def aligned_rows(t: torch.Tensor) -> torch.Tensor:
+    """t contiguous and 16-byte aligned.  A contiguous view can start at any
+    element offset; the owner-computes backward reads grad_output in 16-byte
+    chunks and is taken only for aligned pointers -- it is also the
+    deterministic backward that needs no workspace, so a misaligned view
+    would otherwise be refused there."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone(memory_format=torch.contiguous_format)
+
+
 def backward_raw(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
                  grad_out, fp32_grad_accum: bool, deterministic: bool):
     """One call of ``msda_backward`` (or ``msda_backward_deterministic``) on
     prepared tensors; returns (grad_value, grad_loc, grad_attn)."""
     B, S, M, D = value.shape
     _, Q, _, L, K, _ = sampling_locations.shape
-    grad_out = grad_out.reshape(B, Q, M, D).contiguous()
+    grad_out = aligned_rows(grad_out.reshape(B, Q, M, D))
     lib = _native.load()
     grad_value = torch.empty_like(value)  # written in full by the library
     grad_loc = torch.empty_like(sampling_locations)

@@ -28,3 +28,27 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture
+def overrides():
+    """Setter of library launch overrides (``overrides(BWD_OWNER=0)``, knob
+    names of msda_triton_amd._native.KNOBS); every knob set is restored to
+    the automatic choice when the test ends."""
+    from msda_triton_amd import _native
+
+    touched = []
+
+    def setter(**knobs):
+        lib = _native.load()
+        for name, value in knobs.items():
+            code = _native.KNOBS[name]
+            touched.append(code)
+            _native.check(lib.msda_set_launch_override(code, int(value)),
+                          "msda_set_launch_override")
+
+    yield setter
+    if touched:
+        lib = _native.load()
+        for code in touched:
+            lib.msda_set_launch_override(code, _native.OVERRIDE_AUTO)

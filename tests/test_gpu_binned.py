@@ -12,7 +12,10 @@ accumulation, and the fused front-end -- each against the oracle.
 import pytest
 import torch
 
-from msda_cases import DTYPES, make_inputs
+from msda_cases import DTYPES, _off_knots, make_fused_inputs, make_inputs
+from oracle import run_fused_reference
+from test_gpu_fused import check as check_fused
+from test_gpu_fused import run_fused
 from test_gpu_owner import BINNED, _analytic, check_grads, fwd_bwd, plan, reference_grads
 
 pytestmark = pytest.mark.gpu
@@ -70,15 +73,71 @@ def test_binned_split_bands(dtype):
     check_grads(grads, refs, dtype, sh)
 
 
-def test_binned_against_atomic_path(monkeypatch):
+def test_binned_against_atomic_path(overrides):
     """Encoder-like call: the binned path and the row-dedup atomic path with
     fp32 accumulation agree (same fp32 sums, another order)."""
     case = BIN_CASES[0]
     value, shapes, starts, loc, attn = _inputs(case, torch.float32)
     g1, grads1 = fwd_bwd(value, shapes, starts, loc, attn)
-    monkeypatch.setenv("MSDA_BWD_BIN", "0")
+    overrides(BWD_BIN=0)
     g2, grads2 = fwd_bwd(value, shapes, starts, loc, attn, fp32_grad_accum=True)
     assert torch.equal(g1, g2)
     torch.testing.assert_close(grads1[0], grads2[0], rtol=1e-5, atol=1e-5)
     for a, b in zip(grads1[1:], grads2[1:]):  # same dot products, other lane split
         torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
+
+
+def test_binned_batch_slices_of_at_most_1024_groups():
+    """B*M*L = 1280 (b, m, level) groups: more than one binned launch holds,
+    so the batch runs in slices of 4 + 1 elements (256 groups each), every
+    slice on the binned path with its own bookkeeping.  Tiny maps: the
+    2080 samples of a group pile onto <= 64 pixels (split bands)."""
+    B, Q, M, D, K = 5, 520, 64, 8, 4
+    shapes = [(8, 8), (4, 4), (2, 2), (1, 1)]
+    value, sh, starts, loc, attn = make_inputs(B=B, Q=Q, M=M, D=D, shapes=shapes, K=K,
+                                               dtype=torch.float32, device=DEVICE,
+                                               loc_lo=-0.1, loc_hi=1.1)
+    assert plan(value, loc) == BINNED
+    g, grads = fwd_bwd(value, sh, starts, loc, attn)
+    _, refs = reference_grads(value, sh, loc, attn, g)
+    check_grads(grads, refs, torch.float32, sh)
+
+
+FUSED_BIN_CASE = dict(B=2, Q=600, M=4, D=32, K=4, shapes=[(24, 40), (12, 20), (6, 10)])
+
+
+@pytest.mark.parametrize("per_level", [False, True], ids=["shared_ref", "per_level_ref"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_fused_binned_matches_reference(dtype, per_level):
+    """The fused front-end's binned kernels (offsets from reference points,
+    softmax weights formed from the saved log-sum-exp) against the float64
+    oracle of the composition."""
+    value, shapes, starts, ref, off, logits = make_fused_inputs(
+        **FUSED_BIN_CASE, dtype=dtype, device=DEVICE, per_level=per_level)
+    assert plan(value, off) == BINNED
+    print(f"fused binned {dtype} per_level={per_level}", flush=True)
+    out, g, grads = run_fused(value, shapes, starts, ref, off, logits)
+    ref_out, ref_grads = run_fused_reference(value, shapes, ref, off, logits, g)
+    check_fused(out, grads, ref_out, ref_grads, dtype)
+
+
+@pytest.mark.parametrize("per_level", [False, True], ids=["shared_ref", "per_level_ref"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_fused_binned_split_bands(dtype, per_level):
+    """Reference points N(0.5, 0.01) and offsets N(0, 0.5) px: each (b, m,
+    level)'s 6000 samples land in one or two bands, whose entries are split
+    over several workgroups that add their sums with atomics."""
+    B, Q, M, D, K = 1, 1500, 2, 32, 4
+    shapes = [(40, 60), (20, 30)]
+    value, sh, starts, ref, off, logits = make_fused_inputs(
+        B=B, Q=Q, M=M, D=D, K=K, shapes=shapes, dtype=torch.float32, device="cpu",
+        per_level=per_level, offset_sigma=0.5)
+    gen = torch.Generator().manual_seed(11)
+    ref = (0.5 + 0.01 * torch.randn(ref.shape, generator=gen)).to(dtype)
+    off = _off_knots(off.to(dtype), ref, shapes, per_level)
+    value, ref, off, logits = (t.to(DEVICE, dtype) for t in (value, ref, off, logits))
+    sh, starts = sh.to(DEVICE), starts.to(DEVICE)
+    assert plan(value, off) == BINNED
+    out, g, grads = run_fused(value, sh, starts, ref, off, logits)
+    ref_out, ref_grads = run_fused_reference(value, sh, ref, off, logits, g)
+    check_fused(out, grads, ref_out, ref_grads, dtype)

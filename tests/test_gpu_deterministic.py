@@ -47,12 +47,11 @@ def test_deterministic_matches_reference(case, dtype):
 
 @pytest.mark.parametrize("path", ["owner", "row_dedup", "direct"])
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
-def test_deterministic_is_bitwise_reproducible_under_contention(dtype, path, monkeypatch):
+def test_deterministic_is_bitwise_reproducible_under_contention(dtype, path, overrides):
     """High-contention locations (most samples share a few corners): two
     runs give identical bits; the fp32 result matches float64 closely --
     on the owner path and on the int64 fixed-point atomic paths."""
-    monkeypatch.setenv("MSDA_BWD_OWNER", "1" if path == "owner" else "0")
-    monkeypatch.setenv("MSDA_BWD_PRIV", "0" if path == "direct" else "1")
+    overrides(BWD_OWNER=1 if path == "owner" else 0, BWD_PRIV=0 if path == "direct" else 1)
     value, shapes, starts, _, attn = make_inputs(B=2, Q=120, M=4, D=32, K=4,
                                                  shapes=[(40, 50), (20, 25)], dtype=dtype,
                                                  device=DEVICE)
@@ -145,3 +144,66 @@ def test_deterministic_high_contention_preset_full_size():
     _, refs = run_reference(value, shapes, loc, attn, g, dtype=torch.float64)
     for x, r in zip(g1, refs):
         assert rel_err(x, r) <= BWD_RELERR[torch.bfloat16]
+
+
+@pytest.mark.parametrize("fused", [False, True], ids=["operator", "fused"])
+def test_deterministic_misaligned_grad_out(fused):
+    """grad_output as a contiguous view at an odd element offset (not 16-byte
+    aligned): the deterministic backward of an owner-path call needs no
+    workspace, and the host hands the library an aligned copy, so the call
+    runs and matches the oracle, bit for bit on a second run."""
+    dtype = torch.bfloat16
+    B, Q, M, D, K, shapes_l = 2, 50, 4, 32, 4, [(24, 32), (12, 16), (6, 8)]
+    flat = torch.randn(B * Q * M * D + 1, generator=torch.Generator().manual_seed(7))
+    flat = flat.to(DEVICE, dtype)
+    g = flat[1:].view(B, Q, M * D)
+    assert g.is_contiguous() and g.data_ptr() % 16 != 0
+    runs = []
+    if fused:
+        value, shapes, starts, ref, off, logits = make_fused_inputs(
+            B=B, Q=Q, M=M, D=D, K=K, shapes=shapes_l, dtype=dtype, device=DEVICE, per_level=True)
+        for _ in range(2):
+            leaves = [t.clone().requires_grad_(True) for t in (value, ref, off, logits)]
+            msda_fused(leaves[0], shapes, starts, *leaves[1:], deterministic=True).backward(g)
+            runs.append(tuple(t.grad for t in leaves))
+        _, refs = run_fused_reference(value, shapes, ref, off, logits, g)
+    else:
+        value, shapes, starts, loc, attn = make_inputs(B=B, Q=Q, M=M, D=D, K=K, shapes=shapes_l,
+                                                       dtype=dtype, device=DEVICE)
+        for _ in range(2):
+            runs.append(grads_of(value, shapes, starts, loc, attn, g, deterministic=True)[1])
+        _, refs = run_reference(value, shapes, loc, attn, g, dtype=torch.float64)
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    for x, r in zip(runs[0], refs):
+        assert rel_err(x, r) <= BWD_RELERR[dtype]
+
+
+def test_deterministic_c_abi_misaligned_grad_out_contract():
+    """At the C ABI, a misaligned grad_output rules the owner path out, and
+    the workspace query (0 bytes here) assumes aligned buffers: with no
+    workspace the call is refused before any launch, buffers untouched.
+    (The host operator hands the library aligned copies, see
+    test_deterministic_misaligned_grad_out.)"""
+    from msda_triton_amd import _native
+
+    lib = _native.load()
+    dtype = torch.bfloat16
+    B, Q, M, D, K = 2, 50, 4, 32, 4
+    value, shapes, starts, loc, attn = make_inputs(B=B, Q=Q, M=M, D=D, K=K,
+                                                   shapes=[(24, 32), (12, 16)], dtype=dtype,
+                                                   device=DEVICE)
+    S, L = value.shape[1], 2
+    flat = torch.randn(B * Q * M * D + 1, generator=torch.Generator().manual_seed(3))
+    g_bad = flat.to(DEVICE, dtype)[1:]
+    assert lib.msda_deterministic_workspace_bytes(B, S, M, D, Q, L, K, 2) == 0
+    gv = torch.full_like(value, 3.0)
+    gl, ga = torch.full_like(loc, 3.0), torch.full_like(attn, 3.0)
+    st = torch.cuda.current_stream().cuda_stream
+    rc = lib.msda_backward_deterministic(
+        value.data_ptr(), shapes.data_ptr(), starts.data_ptr(), loc.data_ptr(), attn.data_ptr(),
+        g_bad.data_ptr(), gv.data_ptr(), None, gl.data_ptr(), ga.data_ptr(), B, S, M, D, Q, L, K,
+        2, st)
+    assert rc == 1  # MSDA_ERR_INVALID_ARGUMENT
+    torch.cuda.synchronize()
+    assert bool((gv == 3.0).all()) and bool((gl == 3.0).all()) and bool((ga == 3.0).all())

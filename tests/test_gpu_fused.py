@@ -67,16 +67,18 @@ def test_fused_matches_float64_oracle(case, dtype, per_level):
 
 @pytest.mark.parametrize("priv", ["1", "0", "bin"], ids=["dedup", "direct", "binned"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
-def test_fused_atomic_backward_kernels(dtype, priv, monkeypatch):
+def test_fused_atomic_backward_kernels(dtype, priv, overrides):
     """The other backward kernels (row-dedup and direct atomics, binned
     owner) in their fused variants; the default for these sizes is the
-    owner-computes backward."""
-    monkeypatch.setenv("MSDA_BWD_OWNER", "0")
-    monkeypatch.setenv("MSDA_BWD_BIN", "1" if priv == "bin" else "0")
-    monkeypatch.setenv("MSDA_BWD_PRIV", "0" if priv == "0" else "1")
-    case = FUSED_CASES[0]
+    owner-computes backward.  The binned case uses Q = 400 so that its
+    bookkeeping fits grad_attention_weights in every dtype."""
+    from test_gpu_owner import plan
+
+    overrides(BWD_OWNER=0, BWD_BIN=1 if priv == "bin" else 0, BWD_PRIV=0 if priv == "0" else 1)
+    case = dict(FUSED_CASES[0], Q=400) if priv == "bin" else FUSED_CASES[0]
     value, shapes, starts, ref, off, logits = make_fused_inputs(
         **kw(case), dtype=dtype, device=DEVICE, per_level=True)
+    assert plan(value, off) == {"1": 1, "0": 0, "bin": 3}[priv]
     out, g, grads = run_fused(value, shapes, starts, ref, off, logits)
     ref_out, ref_grads = run_fused_reference(value, shapes, ref, off, logits, g)
     check(out, grads, ref_out, ref_grads, dtype)

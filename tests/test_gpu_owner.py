@@ -8,7 +8,7 @@ that path against the oracle on the cases that stress it -- bands that
 split coarse levels, padded lanes, many samples piled onto one band (more
 CSR entries than one pass holds), level tables other than the cumulative
 one (gaps, overlaps, reordered levels) -- and against the atomic kernels it
-replaces (MSDA_BWD_OWNER=0).
+replaces (override BWD_OWNER=0).
 """
 
 import pytest
@@ -66,11 +66,10 @@ def fwd_bwd(value, shapes, starts, loc, attn, seed=7, **kw):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("owner", ["1", "0", "bin"])
-def test_decoder_shapes_both_paths(dtype, owner, monkeypatch):
+def test_decoder_shapes_both_paths(dtype, owner, overrides):
     """Decoder-style call (Q*K = 1200 per level, coarse levels split into
     several bands) on the owner path, the atomic one and the binned one."""
-    monkeypatch.setenv("MSDA_BWD_OWNER", "1" if owner == "1" else "0")
-    monkeypatch.setenv("MSDA_BWD_BIN", "1" if owner == "bin" else "0")
+    overrides(BWD_OWNER=1 if owner == "1" else 0, BWD_BIN=1 if owner == "bin" else 0)
     value, shapes, starts, loc, attn = make_inputs(
         B=2, Q=300, M=4, D=32, shapes=[(50, 84), (25, 42), (13, 21), (7, 11)], K=4,
         dtype=dtype, device=DEVICE, loc_lo=-0.1, loc_hi=1.1)
@@ -150,13 +149,15 @@ def _analytic(value, shapes, starts, loc, attn, g):
                                   dtype=torch.float64)
 
 
+@pytest.mark.parametrize("path", ["owner", "binned"])
 @pytest.mark.parametrize("layout", ["trailing_rows", "gap_between_levels", "overlapping_levels",
                                     "reversed_levels"])
-def test_nonstandard_level_tables(layout):
+def test_nonstandard_level_tables(layout, path):
     """level_start_index other than the cumulative sum of H*W: value rows no
     level covers must get zero gradient, rows two levels share get both
     levels' contributions.  Checked against the float64 hand backward, which
-    indexes rows through the given starts."""
+    indexes rows through the given starts.  Q = 60 takes the owner path,
+    Q = 600 (Q*K = 2400) the binned one."""
     hw = [(12, 10), (6, 5), (3, 4)]
     sizes = [h * w for h, w in hw]
     if layout == "trailing_rows":
@@ -168,9 +169,10 @@ def test_nonstandard_level_tables(layout):
     else:
         starts, S = [42, 12, 0], 162
     assert all(s + n <= S for s, n in zip(starts, sizes))
-    B, Q, M, D, K = 2, 60, 2, 32, 4
+    B, Q, M, D, K = 2, 60 if path == "owner" else 600, 2, 32, 4
     gen = torch.Generator().manual_seed(5)
-    assert plan(torch.empty(B, S, M, D), torch.empty(B, Q, M, 3, K, 2)) == OWNER
+    want = OWNER if path == "owner" else BINNED
+    assert plan(torch.empty(B, S, M, D), torch.empty(B, Q, M, 3, K, 2)) == want
     value = torch.randn(B, S, M, D, generator=gen)
     loc = -0.1 + 1.2 * torch.rand(B, Q, M, 3, K, 2, generator=gen)
     attn = torch.rand(B, Q, M, 3, K, generator=gen).flatten(3).softmax(-1).view(B, Q, M, 3, K)
@@ -206,7 +208,7 @@ def test_degenerate_levels():
     check_grads(grads, refs, torch.float32, shapes_t)
 
 
-def test_owner_and_atomic_paths_agree_on_decoder_preset(monkeypatch):
+def test_owner_and_atomic_paths_agree_on_decoder_preset(overrides):
     """Full decoder preset (bf16): the owner path (fp32 sums, one rounding)
     against the atomic path with fp32 accumulation -- same fp32 sums up to
     summation order, so they agree to a few bf16 ulps."""
@@ -215,8 +217,7 @@ def test_owner_and_atomic_paths_agree_on_decoder_preset(monkeypatch):
     value, shapes, starts, loc, attn = make_preset_inputs("decoder", device=DEVICE)
     assert plan(value, loc) == OWNER
     g1, grads1 = fwd_bwd(value, shapes, starts, loc, attn)
-    monkeypatch.setenv("MSDA_BWD_OWNER", "0")
-    monkeypatch.setenv("MSDA_BWD_BIN", "0")
+    overrides(BWD_OWNER=0, BWD_BIN=0)
     g2, grads2 = fwd_bwd(value, shapes, starts, loc, attn, fp32_grad_accum=True)
     assert torch.equal(g1, g2)
     for a, b in zip(grads1[1:], grads2[1:]):  # other kernels: same sums, other order

@@ -195,39 +195,36 @@ def test_backward_loc_and_attn_grads_are_deterministic():
 
 
 # ---------------------------------------------------------------------------
-# Every kernel variant: launch-shape overrides (read by the library per call)
+# Every kernel variant: launch-shape overrides (msda_set_launch_override)
 # ---------------------------------------------------------------------------
 
 OVERRIDES = [
     dict(),                                          # defaults: owner backward
-    dict(MSDA_BWD_OWNER="0"),                        # binned owner backward (where it fits)
-    dict(MSDA_BWD_OWNER="0", MSDA_BWD_BIN="0"),      # atomic row-dedup backward
-    dict(MSDA_BWD_OWNER="0", MSDA_BWD_BIN="0", MSDA_BWD_PRIV="0"),  # direct, 16 lanes/row
-    dict(MSDA_BWD_OWNER="0", MSDA_BWD_BIN="0", MSDA_BWD_PRIV="0", MSDA_BWD_CB="16",
-         MSDA_BWD_TS="4"),
-    dict(MSDA_BWD_OWNER="0", MSDA_BWD_BIN="0", MSDA_BWD_PRIV="0", MSDA_BWD_CB="8",
-         MSDA_BWD_TS="16"),
-    dict(MSDA_OWN_MIX="0"),                          # owner path, gradient workgroups last
-    dict(MSDA_OWN_MIX="1"),                          # owner path, gradient workgroups first
-    dict(MSDA_OWN_MIX="-1"),                         # owner path, gradient kernel launched apart
-    dict(MSDA_FWD_TS="1", MSDA_FWD_CB="8"),          # owner path, other dot-kernel shapes
-    dict(MSDA_FWD_TS="1"), dict(MSDA_FWD_TS="16"),
-    dict(MSDA_FWD_CB="8", MSDA_FWD_TS="4"), dict(MSDA_FWD_CB="4", MSDA_FWD_TS="2"),
+    dict(BWD_OWNER=0),                               # binned owner backward (where it fits)
+    dict(BWD_OWNER=0, BWD_BIN=0),                    # atomic row-dedup backward
+    dict(BWD_OWNER=0, BWD_BIN=0, BWD_PRIV=0),        # direct, 16 lanes/row
+    dict(BWD_OWNER=0, BWD_BIN=0, BWD_PRIV=0, BWD_CB=16, BWD_TS=4),
+    dict(BWD_OWNER=0, BWD_BIN=0, BWD_PRIV=0, BWD_CB=8, BWD_TS=16),
+    dict(OWN_MIX=0),                                 # owner path, gradient workgroups last
+    dict(OWN_MIX=1),                                 # owner path, gradient workgroups first
+    dict(OWN_MIX=-1),                                # owner path, gradient kernel launched apart
+    dict(FWD_TS=1, FWD_CB=8),                        # owner path, other dot-kernel shapes
+    dict(FWD_TS=1), dict(FWD_TS=16),
+    dict(FWD_CB=8, FWD_TS=4), dict(FWD_CB=4, FWD_TS=2),
 ]
 
 
 @pytest.fixture
-def env_overrides(request, monkeypatch):
-    for k, v in request.param.items():
-        monkeypatch.setenv(k, v)
+def launch_knobs(request, overrides):
+    overrides(**request.param)
     return request.param
 
 
-@pytest.mark.parametrize("env_overrides", OVERRIDES, indirect=True,
-                         ids=lambda d: ",".join(f"{k[5:]}={v}" for k, v in d.items()) or "default")
+@pytest.mark.parametrize("launch_knobs", OVERRIDES, indirect=True,
+                         ids=lambda d: ",".join(f"{k}={v}" for k, v in d.items()) or "default")
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("case", [CASES[0], CASES[3]], ids=[CASES[0]["id"], CASES[3]["id"]])
-def test_kernel_variants_match_reference(case, dtype, env_overrides):
+def test_kernel_variants_match_reference(case, dtype, launch_knobs):
     value, shapes, starts, loc, attn = make_inputs(**case_kwargs(case), dtype=dtype, device=DEVICE,
                                                    loc_lo=-0.1, loc_hi=1.1)
     out, g, grads = run_fwd_bwd(value, shapes, starts, loc, attn, fp32_grad_accum=True)

@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_strings(lib):
-    assert lib.msda_abi_version() == (1 << 16) | 4
+    assert lib.msda_abi_version() == (1 << 16) | 5
     for code in range(5):
         assert lib.msda_error_string(code)
     assert b"unknown" in lib.msda_error_string(99)
@@ -210,7 +210,7 @@ def test_custom_ops_are_registered_with_fake_shapes():
         assert [t.shape for t in grads] == [value.shape, ref.shape, loc.shape, attn.shape]
 
 
-def test_backward_plan(lib, monkeypatch):
+def test_backward_plan(lib, overrides):
     """Which grad_value path each preset's shapes take (host-only query)."""
     owner, dedup, direct, binned = 2, 1, 0, 3
     # decoder (B4 Q300 L4 K4, bf16): Q*K = 1200 per level, 64-byte rows
@@ -228,7 +228,9 @@ def test_backward_plan(lib, monkeypatch):
     assert lib.msda_backward_plan(2, 21504, 8, 24, 21504, 3, 4, 1, 0) == dedup   # D = 24
     assert lib.msda_backward_plan(2, 21504, 8, 8, 21504, 3, 4, 1, 0) != binned   # 16 B
     assert lib.msda_backward_plan(32, 21504, 8, 32, 21504, 4, 4, 1, 0) == binned  # 1024 groups
-    assert lib.msda_backward_plan(33, 21504, 8, 32, 21504, 4, 4, 1, 0) == dedup
+    # 33 batch elements: slices of at most 1024 groups (32 + 1) stay binned
+    assert lib.msda_backward_plan(33, 21504, 8, 32, 21504, 4, 4, 1, 0) == binned
+    assert lib.msda_backward_plan(1, 21504, 1025, 32, 21504, 1, 4, 1, 0) == dedup
     assert lib.msda_backward_plan(1, 600, 2, 32, 1100, 2, 2, 1, 0) == binned  # 2200 B / group
     assert lib.msda_backward_plan(1, 200000, 2, 32, 1100, 2, 2, 1, 0) == dedup  # bands > room
     # limits of the owner path: Q*K <= 2048, Q*D*elem <= 40960, rows of 16..256 bytes
@@ -242,15 +244,15 @@ def test_backward_plan(lib, monkeypatch):
     assert lib.msda_backward_plan(1, 600, 2, 3, 100, 2, 4, 1, 0) == direct   # odd half row
     assert lib.msda_backward_plan(1, 600, 2, 128, 40, 2, 4, 1, 0) == owner   # 256-byte rows
     assert lib.msda_backward_plan(1, 600, 2, 256, 40, 2, 4, 1, 0) != owner
-    # overrides read per call
-    monkeypatch.setenv("MSDA_BWD_OWNER", "0")
+    # launch overrides
+    overrides(BWD_OWNER=0)
     # decoder: the bookkeeping (2404 B per group) exceeds grad_attention_weights (2400 B)
     assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 0) == dedup
     assert lib.msda_backward_plan(4, 5600, 8, 32, 300, 4, 4, 2, 0) == binned
-    monkeypatch.setenv("MSDA_BWD_BIN", "0")
+    overrides(BWD_BIN=0)
     assert lib.msda_backward_plan(4, 5600, 8, 32, 300, 4, 4, 2, 0) == dedup
     assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 0) == dedup
-    monkeypatch.setenv("MSDA_BWD_PRIV", "0")
+    overrides(BWD_PRIV=0)
     assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 0) == direct
     # errors come back negated
     assert lib.msda_backward_plan(1, 1, 1, 1, 1, 1, 1, 9, 0) == -2
