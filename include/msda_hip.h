@@ -275,6 +275,27 @@ int msda_projection_backward(const void* input, const void* weight, const void* 
                              int64_t out_features, int64_t split, int dtype, void* stream);
 
 /*
+ * msda_projection_backward without the workspace argument: it allocates
+ * nothing.  No counterpart in the reference; it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving or
+ * training loops, harnesses that forbid hipMalloc).  The workspace is a
+ * device array inside the library, 32 MiB per GPU, held by every GPU the
+ * library runs on until the process ends; shapes whose workspace
+ * (msda_projection_workspace_bytes) exceeds it return
+ * MSDA_ERR_UNSUPPORTED_SHAPE.  Every call on one GPU uses that GPU's one
+ * array: calls that overlap on one GPU (other streams, other threads) race
+ * and give wrong results -- serialise them.  Arguments and results as in
+ * msda_projection_backward (bitwise the same outputs).
+ */
+int msda_projection_backward_noalloc(const void* input, const void* weight, const void* weight2,
+                                     const uint8_t* row_mask, const void* grad_output,
+                                     const void* grad_output2, void* grad_input,
+                                     void* grad_weight, void* grad_bias, void* grad_weight2,
+                                     void* grad_bias2, int64_t rows, int64_t in_features,
+                                     int64_t out_features, int64_t split, int dtype,
+                                     void* stream);
+
+/*
  * Human-readable text for a return code (static storage).  The reference has
  * no error channel below Python; this backs the RuntimeError that the host
  * raises for a non-zero code (src/msda_triton/ops.py:165-171 raise the

@@ -2,6 +2,7 @@
 // selection around the kernels in msda_forward.hip / msda_backward.hip.
 // Declarations and the contract live in include/msda_hip.h.
 #include <atomic>
+#include <mutex>
 
 #include "../../include/msda_hip.h"
 #include "msda_launch.h"
@@ -712,6 +713,64 @@ extern "C" int msda_projection_backward(const void* input, const void* weight,
               : nullptr;
   return status(launch_wgrad(dtype, w, grad_weight, two ? grad_weight2 : nullptr, grad_bias,
                              two ? grad_bias2 : nullptr, st));
+}
+
+// ---------------------------------------------------------------------------
+// Projection backward without allocation: the workspace lives in the
+// library's own device memory.
+// ---------------------------------------------------------------------------
+
+// The workspace of msda_projection_backward_noalloc: a file-scope device
+// array, so every GPU the library runs on holds one copy of it from module
+// load until the process ends.  32 MiB covers every half-precision
+// projection the library takes (reductions of at most 512: 17.3 MB at 512 x
+// 512 on 256 CUs) and fp32 ones up to 512 x 512.
+constexpr int64_t kNoAllocScratchBytes = (int64_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// Device address of `scratch` on each device.  In host code the array's
+// name is a host-side stand-in, not a device address: kernels and copies
+// get these addresses, looked up once per device with that device current.
+constexpr int kNoAllocMaxDevices = 64;
+static std::atomic<void*> g_scratch_addr[kNoAllocMaxDevices];
+static std::mutex g_scratch_mu;
+
+static void* scratch_address() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoAllocMaxDevices) return nullptr;
+  void* ptr = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (ptr) return ptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ptr = g_scratch_addr[dev].load(std::memory_order_relaxed);
+  if (!ptr) {
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch_addr[dev].store(ptr, std::memory_order_release);
+  }
+  return ptr;
+}
+
+extern "C" int msda_projection_backward_noalloc(
+    const void* input, const void* weight, const void* weight2, const uint8_t* row_mask,
+    const void* grad_output, const void* grad_output2, void* grad_input, void* grad_weight,
+    void* grad_bias, void* grad_weight2, void* grad_bias2, int64_t rows, int64_t in_features,
+    int64_t out_features, int64_t split, int dtype, void* stream) {
+  const ProjDims d{rows, in_features, out_features, split};
+  const int rc = check_proj(d, dtype);
+  if (rc != MSDA_OK) return rc;
+  const bool two = split < out_features;
+  const bool wgrad = grad_weight || grad_bias || (two && (grad_weight2 || grad_bias2));
+  const bool dx = grad_input != nullptr && rows > 0;
+  void* ws = nullptr;
+  if (dx || wgrad) {
+    if (msda_projection_workspace_bytes(rows, in_features, out_features, dtype) >
+        kNoAllocScratchBytes)
+      return MSDA_ERR_UNSUPPORTED_SHAPE;
+    ws = scratch_address();
+    if (!ws) return MSDA_ERR_LAUNCH;
+  }
+  return msda_projection_backward(input, weight, weight2, row_mask, grad_output, grad_output2,
+                                  grad_input, grad_weight, grad_bias, grad_weight2, grad_bias2, ws,
+                                  rows, in_features, out_features, split, dtype, stream);
 }
 
 extern "C" const char* msda_error_string(int code) {

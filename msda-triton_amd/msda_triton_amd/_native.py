@@ -39,6 +39,7 @@ SIGNATURES = {
     "msda_projection_forward": (_INT, [_P] * 8 + [_I64] * 4 + [_INT, _P]),
     "msda_projection_workspace_bytes": (_I64, [_I64] * 3 + [_INT]),
     "msda_projection_backward": (_INT, [_P] * 12 + [_I64] * 4 + [_INT, _P]),
+    "msda_projection_backward_noalloc": (_INT, [_P] * 11 + [_I64] * 4 + [_INT, _P]),
     "msda_error_string": (ctypes.c_char_p, [_INT]),
     "msda_abi_version": (_INT, []),
     "msda_backward_plan": (_INT, [_I64] * 7 + [_INT, _INT]),
