@@ -11,14 +11,15 @@
 // can be formed by the rows' owners instead:
 //
 //   one workgroup owns (batch b, head m, band [lo, hi) of the pixel axis);
-//   it evaluates the bilinear geometry of every sample of (b, m) on each
-//   level that meets the band (Q * K samples, <= 8 per lane, kept in
-//   registers), counts the in-map corners that land in the band per row
-//   (integer LDS atomics), turns the counts into CSR offsets (block scan),
-//   fills the CSR with (A * w_c, query) entries, and then gives each row to
-//   a team of G lanes that sums its entries' grad_out chunks (staged once in
-//   LDS) in fp32 registers and stores the row -- zeros for rows no sample
-//   touches.
+//   it loads every sample of (b, m) on each level that meets the band (Q *
+//   K samples, <= 8 per lane), keeps those whose corner rows meet the band's
+//   pixel rows (packed into the first lanes, in sample order), evaluates
+//   their bilinear geometry, counts the in-map corners that land in the band
+//   per row (integer LDS atomics), turns the counts into CSR offsets (block
+//   scan), stores zeros for rows no sample touches, fills the CSR with
+//   (A * w_c, query) entries, and then gives each row to a team of G lanes
+//   that sums its entries' grad_out chunks (staged once in LDS) in fp32
+//   registers and stores the row.
 //
 // The sums are the reference's, accumulated in fp32 and rounded once, in
 // every mode (the fp32_grad_accum choice is moot here).  Their order within a
@@ -207,24 +208,39 @@ __device__ __forceinline__ uint32_t own_cell(float x, float y, int W, int H, int
 constexpr int kOwnQBits = 11;  // query index in a CSR entry (Q <= Q * K <= kOwnCap)
 static_assert(kOwnCap <= (1 << kOwnQBits), "query index field");
 
+constexpr int kOwnMaxNs = 8;      // samples per lane and level, at most (Q * K <= 8 * kBlock)
+constexpr int kOwnQueue = 1280;   // compaction: samples moved between lanes per round
+
 // LDS of an owner workgroup.
 template <int kVec, int GB>
 struct OwnLds {
   LevelTable lt;
-  uint16_t s_off[kOwnRows + 8];  // CSR offsets (exclusive prefix sum of the counts)
-  // Entries per row counted per wave (count pass; 16-bit counters, rows 2k
-  // and 2k + 1 in word k), then each wave's exclusive prefix over the
-  // waves; then the CSR entries (A * w_c, query | local row << kOwnQBits),
-  // rows contiguous; then, after the entries are read, each team's piece of
-  // the row it continues from the slice before.
   union {
-    uint32_t cnt[kBlock / kWave][kOwnRows / 2];
-    float2 csr[kOwnCap];
-    float piece[kBlock * kVec];
-  } u;
+    struct {
+      uint16_t s_off[kOwnRows + 8];  // CSR offsets (exclusive prefix sum of the counts)
+      // Entries per row counted per wave (count pass; 16-bit counters, rows
+      // 2k and 2k + 1 in word k), then each wave's exclusive prefix over the
+      // waves; then the CSR entries (A * w_c, query | local row <<
+      // kOwnQBits), rows contiguous; then, after the entries are read, each
+      // team's piece of the row it continues from the slice before.
+      union {
+        uint32_t cnt[kBlock / kWave][kOwnRows / 2];
+        float2 csr[kOwnCap];
+        float piece[kBlock * kVec];
+      } u;
+    } m;
+    // Compaction staging (before the count): kept samples (x, y, A, j) in
+    // their dense order.
+    struct {
+      float4 queue[kOwnQueue];
+    } q;
+  };
   int s_wsum[kBlock / kWave];
+  int s_qc[kOwnMaxNs][kBlock / kWave];  // kept samples per iteration and wave
   alignas(16) uint8_t s_g[GB];  // grad_out rows of (b, m): Q x D * elem
 };
+static_assert(sizeof(float4) * kOwnQueue <= (kOwnRows + 8) * 2 + kOwnCap * 8,
+              "the queue overlays the CSR offsets and counters");
 
 // T: storage dtype; NS: samples per lane and level (NS * kBlock >= Q * K).
 // p.g_rt lanes (a power of two, g_real of them live) cover a value row in
@@ -246,6 +262,7 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
   static_assert(kOwnRows == 8 * kBlock, "eight rows per lane in the scan");
   static_assert(GB % 16 == 0, "whole chunks");
   static_assert(4 * NS * kBlock < 65536, "16-bit CSR offsets");
+  static_assert(NS <= kOwnMaxNs, "compaction counts");
 
   __shared__ union {
     OwnLds<kVec, GB> own;
@@ -266,8 +283,8 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
     return;
   }
   LevelTable& lt = smem.own.lt;
-  uint16_t* const s_off = smem.own.s_off;
-  auto& u = smem.own.u;
+  uint16_t* const s_off = smem.own.m.s_off;
+  auto& u = smem.own.m.u;
   int* const s_wsum = smem.own.s_wsum;
   uint8_t* const s_g = smem.own.s_g;
 
@@ -384,10 +401,96 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
       own_sample<T, FUSED>(p, rs, bq * (uint32_t)p.M + m, (uint32_t)(l * p.K + j) - q * p.K, bq,
                            (uint32_t)l, valid, fw, fh, sx[i], sy[i], sa[i]);
     }
+
+    // 0. Compaction.  A sample can put a corner in the band only if one of
+    // its corner rows y0, y0 + 1 meets the band's pixel rows [ylo, yhi] of
+    // the level -- typically 10-30% of the level's samples.  Those are
+    // packed, in increasing j, into the first npass slots c = tid + i *
+    // kBlock (through LDS), so the count, fill and rank work below runs
+    // over ceil(npass / kBlock) slots instead of NS.  The order (and so
+    // every rank and row sum) stays fixed by the inputs.
+    const int lane = tid & (kWave - 1), wave = tid / kWave;
+    const int ylo = (max(lo, st) - st) / W;
+    const int yhi = (min(hi, st + H * W) - 1 - st) / W;
+    bool keep[NS];
+    uint32_t kpre[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      float y0f, ly;
+      if constexpr (FUSED) {
+        y0f = floorf(sy[i]);
+      } else {
+        coord_cell<T>(sy[i], fh, y0f, ly);
+      }
+      y0f = fminf(fmaxf(y0f, -2.f), fh + 1.f);
+      const int y0 = (int)y0f;  // invalid samples: -2, never kept
+      keep[i] = y0 <= yhi && y0 + 1 >= ylo;
+      const uint64_t bal = __ballot(keep[i]);
+      kpre[i] = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+      if (lane == 0) smem.own.s_qc[i][wave] = (int)__popcll(bal);
+    }
+    __syncthreads();  // counts of kept samples (and, in later rounds, the last pieces read)
+    int npass = 0;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      // slot of this lane's kept sample i: kept samples of the iterations
+      // before, then of the waves before in this iteration, then its lanes'
+      int before_w = 0, all_w = 0;
+#pragma unroll
+      for (int w = 0; w < kBlock / kWave; ++w) {
+        const int c = smem.own.s_qc[i][w];
+        before_w += w < wave ? c : 0;
+        all_w += c;
+      }
+      kpre[i] += (uint32_t)(npass + before_w);
+      npass += all_w;
+    }
+    float cx[NS], cy[NS], ca[NS];
+    uint32_t cj[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      cx[i] = cy[i] = -1e6f;
+      ca[i] = 0.f;
+      cj[i] = 0u;
+    }
+    for (int r0 = 0; r0 < npass; r0 += kOwnQueue) {  // one round unless npass > kOwnQueue
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int pos = (int)kpre[i] - r0;
+        if (keep[i] && pos >= 0 && pos < kOwnQueue)
+          smem.own.q.queue[pos] = make_float4(sx[i], sy[i], sa[i], __int_as_float(tid + i * kBlock));
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int c = tid + i * kBlock;
+        if (c >= r0 && c < r0 + kOwnQueue && c < npass) {
+          const float4 v = smem.own.q.queue[c - r0];
+          cx[i] = v.x;
+          cy[i] = v.y;
+          ca[i] = v.z;
+          cj[i] = (uint32_t)__float_as_int(v.w);
+        }
+      }
+      __syncthreads();  // queue read: its LDS becomes the counters
+    }
+    const int ns_c = (npass + kBlock - 1) / kBlock;  // dense slots in use (uniform)
+
+    if (npass == 0) {  // no sample reaches the band: zeros in the first round
+      if (!written) {
+        const float zero[kVec] = {};
+        for (int r = team; r < nrows; r += kTeams) put(r, zero, false);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      written = true;
+      continue;
+    }
+
 #pragma unroll
     for (int w = 0; w < kBlock / kWave; ++w)
       for (int r = tid; r < (nrows + 1) / 2; r += kBlock) u.cnt[w][r] = 0;
-    __syncthreads();  // counts zeroed (and, in later rounds, the last pieces read)
+    __syncthreads();  // counts zeroed
 
     // 1. Entries per row.  Each wave counts into its own counters, so the
     // count an entry finds -- its rank among the wave's entries of the row
@@ -395,28 +498,33 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
     // ranks (and so the CSR order and every row sum) are the same on every
     // run.  The cells (corner-00 pixel, fractions, in-band corner bits
     // 4i..4i+3) are kept for the fill.
-    const int wave = tid / kWave;
     uint32_t rank[NS * 2];  // 16-bit ranks, corners 2h and 2h + 1 of a sample in word h
     int pix[NS];
     float slx[NS], sly[NS];
     uint32_t bits = 0;
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      const uint32_t bi = own_cell<T, FUSED>(sx[i], sy[i], W, H, st, lo, hi, pix[i], slx[i], sly[i]);
-      bits |= bi << (4 * i);
-      uint32_t rk[4];
+      rank[2 * i] = rank[2 * i + 1] = 0u;
+      pix[i] = 0;
+      slx[i] = sly[i] = 0.f;
+      if (i < ns_c) {
+        const uint32_t bi =
+            own_cell<T, FUSED>(cx[i], cy[i], W, H, st, lo, hi, pix[i], slx[i], sly[i]);
+        bits |= bi << (4 * i);
+        uint32_t rk[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        rk[c] = 0;
-        if (bi & (1u << c)) {
-          // A wave adds at most 64 * NS < 2^16 to a row: no carry between halves.
-          const int r = pix[i] + (c & 1) + (c >> 1) * W - lo;
-          const uint32_t sh = (uint32_t)(r & 1) * 16u;
-          rk[c] = (atomicAdd(&u.cnt[wave][r >> 1], 1u << sh) >> sh) & 0xffffu;
+        for (int c = 0; c < 4; ++c) {
+          rk[c] = 0;
+          if (bi & (1u << c)) {
+            // A wave adds at most 64 * NS < 2^16 to a row: no carry between halves.
+            const int r = pix[i] + (c & 1) + (c >> 1) * W - lo;
+            const uint32_t sh = (uint32_t)(r & 1) * 16u;
+            rk[c] = (atomicAdd(&u.cnt[wave][r >> 1], 1u << sh) >> sh) & 0xffffu;
+          }
         }
+        rank[2 * i] = rk[0] | rk[1] << 16;
+        rank[2 * i + 1] = rk[2] | rk[3] << 16;
       }
-      rank[2 * i] = rk[0] | rk[1] << 16;
-      rank[2 * i + 1] = rk[2] | rk[3] << 16;
     }
     __syncthreads();
 
@@ -454,20 +562,37 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
     }
     __syncthreads();
 
+    // Rows without entries: zeros in the first round (untouched in later
+    // ones), stored now so that the writes drain while the CSR is filled
+    // and summed.  Four rows per team and step, their offsets read together.
+    if (!written) {
+      const float zero[kVec] = {};
+      for (int rb = team * 4; rb < nrows; rb += kTeams * 4) {
+        int o[5];
+#pragma unroll
+        for (int k = 0; k < 5; ++k) o[k] = s_off[min(rb + k, nrows)];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (rb + k < nrows && o[k + 1] == o[k]) put(rb + k, zero, false);
+      }
+    }
+
     // An entry's rank in its row: the entries of the waves before it, then
     // its rank within its wave.
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      int before[4];
+      if (i < ns_c) {
+        int before[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const bool in = (bits >> (4 * i + c)) & 1u;
-        const int r = in ? pix[i] + (c & 1) + (c >> 1) * W - lo : 0;
-        before[c] = (int)((u.cnt[wave][r >> 1] >> ((r & 1) * 16)) & 0xffffu);
-        if (!in) before[c] = 0;
+        for (int c = 0; c < 4; ++c) {
+          const bool in = (bits >> (4 * i + c)) & 1u;
+          const int r = in ? pix[i] + (c & 1) + (c >> 1) * W - lo : 0;
+          before[c] = (int)((u.cnt[wave][r >> 1] >> ((r & 1) * 16)) & 0xffffu);
+          if (!in) before[c] = 0;
+        }
+        rank[2 * i] += (uint32_t)before[0] | (uint32_t)before[1] << 16;
+        rank[2 * i + 1] += (uint32_t)before[2] | (uint32_t)before[3] << 16;
       }
-      rank[2 * i] += (uint32_t)before[0] | (uint32_t)before[1] << 16;
-      rank[2 * i + 1] += (uint32_t)before[2] | (uint32_t)before[3] << 16;
     }
     __syncthreads();  // counters read: the CSR reuses them
 
@@ -497,11 +622,12 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
       // registers).
 #pragma unroll
       for (int i = 0; i < NS; ++i)
-        asm volatile("" : "+v"(pix[i]), "+v"(slx[i]), "+v"(sly[i]), "+v"(sa[i]));
+        asm volatile("" : "+v"(pix[i]), "+v"(slx[i]), "+v"(sly[i]), "+v"(ca[i]), "+v"(cj[i]));
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
+        if (i >= ns_c) continue;
         const float lx = slx[i], ly = sly[i];
-        const uint32_t q = fdiv((uint32_t)min(tid + i * kBlock, nsmp - 1), p.div_k);
+        const uint32_t q = fdiv(cj[i], p.div_k);
         const float mx = 1.f - lx, my = 1.f - ly;
         // The four row offsets are read unconditionally (row 0 stands in
         // for corners that add nothing) so that they share one LDS wait.
@@ -518,25 +644,11 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
           if (in[c]) {
             const float w = (c & 1 ? lx : mx) * (c >> 1 ? ly : my);
             const int slot = o[c] - base + (int)((rank[2 * i + (c >> 1)] >> (16 * (c & 1))) & 0xffffu);
-            u.csr[slot] = make_float2(sa[i] * w, __int_as_float((int)q | r[c] << kOwnQBits));
+            u.csr[slot] = make_float2(ca[i] * w, __int_as_float((int)q | r[c] << kOwnQBits));
           }
         }
       }
       __syncthreads();
-
-      // Rows without entries: zeros in the first round, untouched later.
-      // Four rows per team and step, their offsets read together.
-      if (!written) {
-        const float zero[kVec] = {};
-        for (int rb = r0 + team * 4; rb < r1; rb += kTeams * 4) {
-          int o[5];
-#pragma unroll
-          for (int k = 0; k < 5; ++k) o[k] = s_off[min(rb + k, r1)];
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-            if (rb + k < r1 && o[k + 1] == o[k]) put(rb + k, zero, false);
-        }
-      }
 
       // Entries: team t sums slice [t * cs, (t + 1) * cs) of the CSR.  A row
       // whose entries all lie in the slice is stored by the team; the piece
