@@ -187,26 +187,63 @@ __global__ __launch_bounds__(kBlock) void cast_kernel(const float* src, void* ds
 // integer atomicMax gives the exact maximum whatever the order.  Atomics on
 // one address serialise at the memory side, so each workgroup reduces first
 // (wave xor butterfly, then LDS) and issues one atomic per word.
+// max |x| over n elements of T at base, this thread's share (thread t of
+// nt): element-wise up to the first 16-byte boundary, then 16-byte loads,
+// four in flight per thread, then the tail.
+template <class T>
+__device__ __forceinline__ float absmax_range(const void* base, uint64_t n, uint64_t t,
+                                              uint64_t nt) {
+  float m = 0.f;
+  if (base == nullptr || n == 0) return m;
+  constexpr int kE = 16 / T::kBytes;  // elements per 16 bytes
+  uint64_t head = ((16u - (reinterpret_cast<uintptr_t>(base) & 15u)) & 15u) / T::kBytes;
+  if (head > n) head = n;
+  for (uint64_t i = t; i < head; i += nt) m = fmaxf(m, fabsf(load1<T>(base, i)));
+  const uint64_t nv = (n - head) / kE;
+  const uint4* v = reinterpret_cast<const uint4*>(static_cast<const char*>(base) + head * T::kBytes);
+  for (uint64_t i = t; i < nv; i += 4 * nt) {
+    uint4 x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = i + u * nt < nv ? v[i + u * nt] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if constexpr (T::kBytes == 4) {
+          m = fmaxf(m, fabsf(__uint_as_float(w[k])));
+        } else {
+          float lo, hi;
+          unpack2<T>(w[k], lo, hi);
+          m = fmaxf(m, fmaxf(fabsf(lo), fabsf(hi)));
+        }
+      }
+    }
+  }
+  for (uint64_t i = head + nv * kE + t; i < n; i += nt) m = fmaxf(m, fabsf(load1<T>(base, i)));
+  return m;
+}
+
 template <class T>
 __global__ __launch_bounds__(kBlock) void det_max_kernel(const void* attn, uint64_t n_attn,
                                                          const void* gout, uint64_t n_gout,
                                                          uint32_t* det_max) {
   __shared__ float s_m[2][kBlock / kWave];
-  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  const uint64_t nt = (uint64_t)gridDim.x * kBlock;
   const uint64_t t0 = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  float ma = 0.f, mg = 0.f;
-  for (uint64_t i = t0; i < n_attn; i += stride) ma = fmaxf(ma, fabsf(load1<T>(attn, i)));
-  for (uint64_t i = t0; i < n_gout; i += stride) mg = fmaxf(mg, fabsf(load1<T>(gout, i)));
+  float ma = absmax_range<T>(attn, n_attn, t0, nt);
+  const float mg = absmax_range<T>(gout, n_gout, t0, nt);
   if (attn == nullptr) ma = 1.f;
+  float mgr = mg;
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
     ma = fmaxf(ma, __shfl_xor(ma, d));
-    mg = fmaxf(mg, __shfl_xor(mg, d));
+    mgr = fmaxf(mgr, __shfl_xor(mgr, d));
   }
   const int wave = threadIdx.x / kWave;
   if (threadIdx.x % kWave == 0) {
     s_m[0][wave] = ma;
-    s_m[1][wave] = mg;
+    s_m[1][wave] = mgr;
   }
   __syncthreads();
   if (threadIdx.x < 2) {

@@ -15,25 +15,31 @@
 // band of pk puts every sample that can touch band j in the keys
 // band((j P - W - 1)+) .. j, which are contiguous once the samples are
 // sorted by key.  Four launches:
-//   bin_kernel<count>  per-band sample counts (LDS histogram, one global add
-//                      per band and workgroup);
-//   bin_scan_kernel    per-group exclusive prefix -> each band's first entry
-//                      (the fill cursors), and the work items: each band's
-//                      entry range in chunks of at most `chunk` entries;
-//   bin_kernel<fill>   writes each sample's id (q * K + k) at its band's
-//                      cursor (LDS ranks + one global add per band);
+//   bin_count_kernel   per block of 4096 samples, its count per key (LDS
+//                      histogram), one row of a count matrix;
+//   bin_scan_kernel    per group: each block's exclusive prefix within each
+//                      key, the key cursors (exclusive prefix over the keys)
+//                      and the work items: each band's entry range in chunks
+//                      of at most `chunk` entries;
+//   bin_fill_kernel    writes each sample's id (q * K + k) at a slot fixed
+//                      by the inputs (cursor + earlier blocks + earlier
+//                      waves + per-wave LDS rank): a key's entries are in
+//                      sample order, so grouped by query;
 //   bin_acc_kernel     per work item: the entries' corner contributions to
 //                      the band's rows are summed in fp32 registers, then
 //                      the band is stored (its only item) or added with
 //                      buffer atomics (items of a band split in chunks, or
 //                      any band when the level table lets levels share rows).
 // No workspace: the entry lists live in grad_sampling_locations (4 bytes per
-// sample, its size at least) and the counts, cursors and items in
+// sample, its size at least) and the cursors and items in
 // grad_attention_weights, both written in full afterwards by the gradient
-// kernel.  grad_value (or the fp32 scratch) is zero-filled beforehand.
-// Entry order within a band depends on the global adds' order, so the fp32
-// sums (and grad_value) are not bitwise reproducible; the deterministic
-// entry points do not use this path.
+// kernel; the count matrix lives in the accumulator (grad_value or the fp32
+// scratch), which is zero-filled after the binning.  Entry order and the
+// order of every fp32 sum within a work item are fixed by the inputs; bands
+// split over several items add their partial sums with float atomics, whose
+// order varies.  The deterministic entry points accumulate in int64 fixed
+// point instead (each item's fp32 sums converted, then stored or added
+// exactly), so their grad_value is bitwise reproducible.
 #include "msda_launch.h"
 
 #include <atomic>
@@ -42,8 +48,10 @@ namespace msda {
 
 namespace {
 
-constexpr int kBinPerThread = 4;
-constexpr int kBinPerWg = kBinPerThread * kBlock;  // samples per binning workgroup
+constexpr int kBinPerWave = 1024;                            // samples per wave (contiguous)
+constexpr int kBinPerWg = kBinPerWave * (kBlock / kWave);    // samples per binning workgroup
+constexpr int kBinIt = kBinPerWave / kWave;                  // samples per lane
+constexpr int kBinXcds = 8;                                  // item counters (one per XCD)
 
 // Cell of a sample, as make_sample_at forms it (same clamps): (x, y) is the
 // location, or (FUSED) the offset in level pixels from reference point
@@ -168,88 +176,181 @@ __device__ __forceinline__ GroupLevel group_level(const Params& p, const BinArgs
   return r;
 }
 
-// FILL == false: per-band counts; true: entries at the band cursors.
-template <class T, bool FUSED, bool FILL>
-__global__ __launch_bounds__(kBlock) void bin_kernel(Params p, BinArgs a) {
-  __shared__ uint32_t s_hist[kBinMaxBands];
-  __shared__ uint32_t s_base[FILL ? kBinMaxBands : 1];
-  const int g = blockIdx.x / a.nqb;
-  const int qb = blockIdx.x - g * a.nqb;
-  const GroupLevel gl = group_level(p, a, g);
-  if (gl.nk <= 0) return;
-  for (int j = threadIdx.x; j < gl.nk; j += kBlock) s_hist[j] = 0u;
-  __syncthreads();
-
+// Key of each of this lane's kBinIt samples of group g, sample block qb:
+// sample li = qb * kBinPerWg + wave * kBinPerWave + u * kWave + lane (a
+// wave's samples are one contiguous run, in sample order), key = 2^log2k
+// pixel block of the first in-map corner, ~0 for a sample with no corner in
+// the map (or past the last sample).
+template <class T, bool FUSED>
+__device__ __forceinline__ void bin_keys(const Params& p, const BinArgs& a, const GroupLevel& gl,
+                                         int qb, uint32_t (&key)[kBinIt]) {
   const uint32_t qk = (uint32_t)(p.Q * p.K);
   const BinSrc rs = bin_src(p, a);
   const float fw = (float)gl.W, fh = (float)gl.H;
-  uint32_t key[kBinPerThread], rank[kBinPerThread], lid[kBinPerThread];
+  const uint32_t li0 = (uint32_t)qb * kBinPerWg + (threadIdx.x / kWave) * kBinPerWave +
+                       (threadIdx.x & (kWave - 1));
+  BinIn in[kBinIt];
 #pragma unroll
-  for (int u = 0; u < kBinPerThread; ++u) {
-    const uint32_t li = (uint32_t)qb * kBinPerWg + u * kBlock + threadIdx.x;
-    lid[u] = li;
-    key[u] = ~0u;
-    rank[u] = 0u;
+  for (int u = 0; u < kBinIt; ++u) {  // all loads in flight together
+    const uint32_t li = li0 + u * kWave;
+    in[u] = BinIn{0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (li < qk) {
       const uint32_t q = fdiv(li, p.div_k), k = li - q * (uint32_t)p.K;
       const uint32_t bq = (uint32_t)gl.b * p.Q + q;
       const uint32_t pair = bq * p.M + gl.m;
       const uint32_t pi = pair * (uint32_t)p.LK + (uint32_t)gl.l * p.K + k;
-      const BinIn in = bin_load<T, FUSED, false>(p, rs, bq, pair, pi, gl.l);
+      in[u] = bin_load<T, FUSED, false>(p, rs, bq, pair, pi, gl.l);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kBinIt; ++u) {
+    const uint32_t li = li0 + u * kWave;
+    key[u] = ~0u;
+    if (li < qk) {
       int32_t x0, y0;
       float lx, ly;
-      bin_cell<T, FUSED>(in.x, in.y, in.rx, in.ry, fw, fh, x0, y0, lx, ly);
+      bin_cell<T, FUSED>(in[u].x, in[u].y, in[u].rx, in[u].ry, fw, fh, x0, y0, lx, ly);
       const uint32_t vm = bin_vmask(x0, y0, gl.H, gl.W);
       if (vm) {
         const int32_t c = __builtin_ctz(vm);
         const int32_t pk = y0 * gl.W + x0 + ((c & 1) ? 1 : 0) + ((c & 2) ? gl.W : 0);
         key[u] = (uint32_t)pk >> a.log2k;
-        rank[u] = atomicAdd(&s_hist[key[u]], 1u);
-      }
-    }
-  }
-  __syncthreads();
-  uint32_t* const counts = (FILL ? a.cursors : a.counts) + (uint32_t)g * a.nbmax;
-  for (int j = threadIdx.x; j < gl.nk; j += kBlock) {
-    const uint32_t h = s_hist[j];
-    if (h == 0u) continue;
-    if constexpr (FILL) {
-      s_base[j] = atomicAdd(&counts[j], h);
-    } else {
-      atomicAdd(&counts[j], h);
-    }
-  }
-  if constexpr (FILL) {
-    __syncthreads();
-    uint32_t* const ent = a.entries + (uint64_t)g * qk;
-#pragma unroll
-    for (int u = 0; u < kBinPerThread; ++u) {
-      if (key[u] != ~0u) {
-        const uint32_t pos = s_base[key[u]] + rank[u];
-        if (pos < qk) ent[pos] = lid[u];
       }
     }
   }
 }
 
-// One workgroup per group: cursors = exclusive prefix of the counts, then
-// the work items (band | several << 31, first entry, end entry, 0).
+// Group and sample block of a binning workgroup.  Each XCD takes a
+// contiguous range of (b, m, sample block, level) with the level fastest:
+// the L levels' samples of a query share the parameter lines its XCD's L2
+// holds (a pair's L * K locations are one run).
+__device__ __forceinline__ void bin_block(const Params& p, const BinArgs& a, int& g, int& qb) {
+  const int lb = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int l = lb % p.L;
+  const int t = lb / p.L;
+  qb = t % a.nqb;
+  g = (t / a.nqb) * p.L + l;
+}
+
+// Per sample block: its samples' count per key, one row of the group's
+// count matrix a.mat (every key written, so no zero-fill is needed).
+template <class T, bool FUSED>
+__global__ __launch_bounds__(kBlock) void bin_count_kernel(Params p, BinArgs a) {
+  __shared__ uint32_t s_hist[kBinMaxBands];
+  int g, qb;
+  bin_block(p, a, g, qb);
+  const GroupLevel gl = group_level(p, a, g);
+  if (gl.nk <= 0) return;
+  for (int j = threadIdx.x; j < gl.nk; j += kBlock) s_hist[j] = 0u;
+  __syncthreads();
+  uint32_t key[kBinIt];
+  bin_keys<T, FUSED>(p, a, gl, qb, key);
+#pragma unroll
+  for (int u = 0; u < kBinIt; ++u)
+    if (key[u] != ~0u) atomicAdd(&s_hist[key[u]], 1u);
+  __syncthreads();
+  uint32_t* const row = a.mat + ((uint64_t)g * a.nqb + qb) * a.nbmax;
+  for (int j = threadIdx.x; j < gl.nk; j += kBlock) row[j] = s_hist[j];
+}
+
+// Per sample block: each sample's entry id (q * K + k) at its slot.  The
+// slot of a sample is fixed by the inputs: key cursor (entries of the
+// group's earlier keys) + entries of the key from earlier sample blocks
+// (a.mat after bin_scan_kernel) + entries of the key from earlier waves of
+// the block + the sample's rank among its wave's samples of the key.  The
+// last comes from per-wave LDS counters, whose returned values depend only
+// on the wave's own instructions in program order.  So a key's entries are
+// in sample order block by block, wave by wave: grouped by query, which
+// the accumulation kernel's loads of grad_out rows and parameters rely on.
+template <class T, bool FUSED>
+__global__ __launch_bounds__(kBlock) void bin_fill_kernel(Params p, BinArgs a) {
+  // 16-bit counters per wave, keys 2k and 2k + 1 in word k (a wave adds at
+  // most kBinPerWave < 2^16 to a key), then each wave's exclusive prefix
+  // over the waves before it.
+  __shared__ uint32_t s_cnt[kBlock / kWave][kBinMaxBands / 2];
+  __shared__ uint32_t s_base[kBinMaxBands];
+  int g, qb;
+  bin_block(p, a, g, qb);
+  const GroupLevel gl = group_level(p, a, g);
+  if (gl.nk <= 0) return;
+  const int nwd = (gl.nk + 1) / 2;
+  const int wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int w = 0; w < kBlock / kWave; ++w)
+    for (int j = threadIdx.x; j < nwd; j += kBlock) s_cnt[w][j] = 0u;
+  const uint32_t* const row = a.mat + ((uint64_t)g * a.nqb + qb) * a.nbmax;
+  const uint32_t* const cur = a.cursors + (uint32_t)g * a.nbmax;
+  for (int j = threadIdx.x; j < gl.nk; j += kBlock) s_base[j] = cur[j] + row[j];
+  __syncthreads();
+  uint32_t key[kBinIt], rank[kBinIt];
+  bin_keys<T, FUSED>(p, a, gl, qb, key);
+#pragma unroll
+  for (int u = 0; u < kBinIt; ++u) {
+    rank[u] = 0u;
+    if (key[u] != ~0u) {
+      const uint32_t sh = (key[u] & 1u) * 16u;
+      rank[u] = (atomicAdd(&s_cnt[wave][key[u] >> 1], 1u << sh) >> sh) & 0xffffu;
+    }
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < nwd; j += kBlock) {
+    uint32_t c = 0u;  // both halves at once: no half exceeds 2^16
+#pragma unroll
+    for (int w = 0; w < kBlock / kWave; ++w) {
+      const uint32_t n = s_cnt[w][j];
+      s_cnt[w][j] = c;
+      c += n;
+    }
+  }
+  __syncthreads();
+  const uint32_t qk = (uint32_t)(p.Q * p.K);
+  uint32_t* const ent = a.entries + (uint64_t)g * qk;
+  const uint32_t li0 = (uint32_t)qb * kBinPerWg + wave * kBinPerWave + (threadIdx.x & (kWave - 1));
+#pragma unroll
+  for (int u = 0; u < kBinIt; ++u) {
+    if (key[u] != ~0u) {
+      const uint32_t k = key[u];
+      const uint32_t before = (s_cnt[wave][k >> 1] >> ((k & 1u) * 16u)) & 0xffffu;
+      const uint32_t pos = s_base[k] + before + rank[u];
+      if (pos < qk) ent[pos] = li0 + u * kWave;
+    }
+  }
+}
+
+// One workgroup per group: each key's total over the sample blocks, the
+// count matrix turned into each block's exclusive prefix within the key,
+// the key cursors (exclusive prefix of the totals over the keys), then the
+// work items (band | several << 31, first entry, end entry, 0).
 __global__ __launch_bounds__(kBlock) void bin_scan_kernel(Params p, BinArgs a) {
   __shared__ uint32_t s_off[kBinMaxBands + 1];
   __shared__ uint32_t s_scan[kBlock];
   const int g = blockIdx.x;
-  if (g == 0 && threadIdx.x == 0) *a.next = 0u;
+  if (g == 0 && threadIdx.x < kBinXcds) a.next[threadIdx.x] = 0u;
   const GroupLevel gl = group_level(p, a, g);
   if (gl.nk <= 0) {
     if (threadIdx.x == 0) a.nitems[g] = 0u;
     return;
   }
-  const uint32_t* counts = a.counts + (uint32_t)g * a.nbmax;
+  uint32_t* const mat = a.mat + (uint64_t)g * a.nqb * a.nbmax;
   uint32_t* cursors = a.cursors + (uint32_t)g * a.nbmax;
   uint32_t carry = 0u, total = 0u;
   for (int j0 = 0; j0 < gl.nk; j0 += kBlock) {
     const int j = j0 + threadIdx.x;
-    const uint32_t v = j < gl.nk ? counts[j] : 0u;
+    uint32_t v = 0u;
+    if (j < gl.nk) {
+      // The key's column, eight blocks' loads in flight at a time.
+      for (int qb0 = 0; qb0 < a.nqb; qb0 += 8) {
+        uint32_t n[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          n[i] = qb0 + i < a.nqb ? mat[(uint64_t)(qb0 + i) * a.nbmax + j] : 0u;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (qb0 + i < a.nqb) mat[(uint64_t)(qb0 + i) * a.nbmax + j] = v;
+          v += n[i];
+        }
+      }
+    }
     const uint32_t ex = block_excl_scan(v, s_scan, total);
     if (j < gl.nk) {
       s_off[j] = carry + ex;
@@ -336,7 +437,7 @@ __global__ __launch_bounds__(kBlock, 3) void bin_acc_kernel(Params p, BinArgs a)
   constexpr int kStride = kD + 1;     // LDS row stride (floats): spreads teams over banks
   static_assert(kD <= kWave && (kD & (kD - 1)) == 0, "team of D lanes");
   constexpr int kP = kBinAccFloats / kD;  // rows per band
-  constexpr int kPerT = (kP + kBlock - 1) / kBlock;
+  constexpr int kWPT = (kP / 2 + kBlock - 1) / kBlock;  // counter words per thread
   // Thread-owned accumulators: kChT channels of kRowsT rows (32 floats);
   // 8 channels each, so that the entries of a busy row are split over
   // several threads.
@@ -351,13 +452,21 @@ __global__ __launch_bounds__(kBlock, 3) void bin_acc_kernel(Params p, BinArgs a)
   i32x4* const s_g = s_u;
   float* const s_acc = reinterpret_cast<float*>(s_u);
   __shared__ float4 s_coef[kBlock];   // A * w_c
-  __shared__ uint32_t s_cnt[kP];      // corner entries per band row (this round)
-  __shared__ uint32_t s_off[kP + 1];  // their exclusive prefix
+  // Corner entries per band row counted per wave (this round; 16-bit, rows
+  // 2k and 2k + 1 in word k), then each wave's exclusive prefix over the
+  // waves before it: an entry's rank in its row depends only on the
+  // inputs, so the order of every fp32 sum is fixed.
+  __shared__ uint32_t s_cnt[kBlock / kWave][kP / 2];
+  __shared__ uint32_t s_off[kP + 1];  // row offsets: exclusive prefix of the row totals
   __shared__ uint16_t s_ent[4 * kBlock];  // entries by row: staged sample * 4 + corner
   __shared__ uint32_t s_wsum[kBlock / kWave];
   __shared__ uint32_t s_pre[kBinMaxGroups + 1];
   __shared__ uint32_t s_scan[kBlock];
-  for (int i = threadIdx.x; i < kP; i += kBlock) s_cnt[i] = 0u;
+  static_assert(kP % 2 == 0, "two rows per counter word");
+#pragma unroll
+  for (int w = 0; w < kBlock / kWave; ++w)
+    for (int i = threadIdx.x; i < kP / 2; i += kBlock) s_cnt[w][i] = 0u;
+  const int wave = threadIdx.x / kWave;
 
   // Item prefix over the groups.
   {
@@ -379,23 +488,35 @@ __global__ __launch_bounds__(kBlock, 3) void bin_acc_kernel(Params p, BinArgs a)
     if (threadIdx.x == 0) s_pre[a.ngroups] = total;
     __syncthreads();
   }
-  const uint32_t ntot = s_pre[a.ngroups];
   const uint32_t qk = (uint32_t)(p.Q * p.K);
   const uint32_t P = 1u << a.log2p;
   const BinSrc rs = bin_src(p, a);
   const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.grad_out, p.gout_bytes);
   const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.grad_acc, p.acc_bytes);
+  const float det_s = A::kBytes == 8 ? det_scale(p) : 0.f;  // int64 fixed-point scale
 
+  // Items by XCD: XCD x owns the items of groups [x ng / 8, (x + 1) ng / 8)
+  // -- whole (b, m) runs of levels, whose items share grad_out rows and
+  // parameter lines in that XCD's L2 -- and its workgroups (block ids x, x
+  // + 8, ...) take them in order from counter x; then they help the other
+  // XCDs' lists in turn.  Every workgroup's loop ends once all eight
+  // counters have passed their lists' ends.
   __shared__ uint32_t s_w;
+  const int xcd = (int)(blockIdx.x % kBinXcds);
+  int src = 0;
   for (;;) {
-    // Next item from the global counter (every workgroup's loop ends once
-    // the counter passes the item count).
-    if (threadIdx.x == 0) s_w = atomicAdd(a.next, 1u);
+    const int xs = (xcd + src) % kBinXcds;
+    const int g0 = xs * a.ngroups / kBinXcds, g1 = (xs + 1) * a.ngroups / kBinXcds;
+    const uint32_t end = s_pre[g1];
+    if (threadIdx.x == 0) s_w = s_pre[g0] < end ? s_pre[g0] + atomicAdd(&a.next[xs], 1u) : end;
     __syncthreads();
     const uint32_t w = s_w;
     __syncthreads();
-    if (w >= ntot) break;
-    int lo = 0, hi = a.ngroups;  // s_pre[lo] <= w < s_pre[hi]
+    if (w >= end) {
+      if (++src == kBinXcds) break;
+      continue;
+    }
+    int lo = g0, hi = g1;  // s_pre[lo] <= w < s_pre[hi]
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
       if (s_pre[mid] <= w) lo = mid; else hi = mid;
@@ -459,7 +580,8 @@ __global__ __launch_bounds__(kBlock, 3) void bin_acc_kernel(Params p, BinArgs a)
         for (int c = 0; c < 4; ++c) {
           if (((vm >> c) & 1u) && rr[c] >= 0 && rr[c] < nrow) {
             rw[c] = (uint32_t)rr[c];
-            rk[c] = atomicAdd(&s_cnt[rw[c]], 1u);
+            const uint32_t sh = (rw[c] & 1u) * 16u;  // a wave adds at most 4 * 64 to a row
+            rk[c] = (atomicAdd(&s_cnt[wave][rw[c] >> 1], 1u << sh) >> sh) & 0xffffu;
           }
         }
         const float mx = 1.f - lx, my = 1.f - ly;
@@ -474,15 +596,28 @@ __global__ __launch_bounds__(kBlock, 3) void bin_acc_kernel(Params p, BinArgs a)
       id_next = load_id(rb + 2 * kBlock + threadIdx.x);
       __syncthreads();
 
-      // Row offsets: exclusive prefix of the counts (which are reset).
+      // Row offsets: exclusive prefix of the row totals; each wave's counter
+      // becomes the entries of the waves before it.  A thread takes kWPT
+      // counter words (rows 2 wd, 2 wd + 1), both halves summed at once: a
+      // row takes at most one corner of each of the round's samples, so no
+      // half exceeds 2^16.
       {
-        uint32_t v[kPerT], sum = 0u;
+        uint32_t v[2 * kWPT], sum = 0u;
 #pragma unroll
-        for (int i = 0; i < kPerT; ++i) {
-          const int r = threadIdx.x * kPerT + i;
-          v[i] = r < kP ? s_cnt[r] : 0u;
-          if (r < kP) s_cnt[r] = 0u;
-          sum += v[i];
+        for (int i = 0; i < kWPT; ++i) {
+          const int wd = threadIdx.x * kWPT + i;
+          uint32_t c = 0u;
+          if (wd < kP / 2) {
+#pragma unroll
+            for (int w = 0; w < kBlock / kWave; ++w) {
+              const uint32_t n = s_cnt[w][wd];
+              s_cnt[w][wd] = c;
+              c += n;
+            }
+          }
+          v[2 * i] = c & 0xffffu;
+          v[2 * i + 1] = c >> 16;
+          sum += v[2 * i] + v[2 * i + 1];
         }
         const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
         uint32_t x = sum;
@@ -501,8 +636,8 @@ __global__ __launch_bounds__(kBlock, 3) void bin_acc_kernel(Params p, BinArgs a)
           tot += ws;
         }
 #pragma unroll
-        for (int i = 0; i < kPerT; ++i) {
-          const int r = threadIdx.x * kPerT + i;
+        for (int i = 0; i < 2 * kWPT; ++i) {
+          const int r = threadIdx.x * 2 * kWPT + i;
           if (r < kP) s_off[r] = ex;
           ex += v[i];
         }
@@ -511,8 +646,16 @@ __global__ __launch_bounds__(kBlock, 3) void bin_acc_kernel(Params p, BinArgs a)
       }
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        if (rw[c] != 0xffffu) s_ent[s_off[rw[c]] + rk[c]] = (uint16_t)(threadIdx.x * 4 + c);
+        if (rw[c] != 0xffffu) {
+          const uint32_t before = (s_cnt[wave][rw[c] >> 1] >> ((rw[c] & 1u) * 16u)) & 0xffffu;
+          s_ent[s_off[rw[c]] + before + rk[c]] = (uint16_t)(threadIdx.x * 4 + c);
+        }
       __syncthreads();
+      // Counters reset for the next round (it counts after this round's
+      // closing barrier).
+#pragma unroll
+      for (int w = 0; w < kBlock / kWave; ++w)
+        for (int i = threadIdx.x; i < kP / 2; i += kBlock) s_cnt[w][i] = 0u;
 
       // Each thread adds the entries of the rows it owns to its registers.
       const float* coefs = reinterpret_cast<const float*>(s_coef);
@@ -580,7 +723,20 @@ __global__ __launch_bounds__(kBlock, 3) void bin_acc_kernel(Params p, BinArgs a)
       const int row = idx / kD, c0 = idx % kD;
       const float v0 = s_acc[row * kStride + c0], v1 = s_acc[row * kStride + c0 + 1];
       const uint32_t el = vrow0 + (uint32_t)row * vstep + c0;
-      if (!several) {
+      if constexpr (A::kBytes == 8) {
+        // Deterministic: the item's fp32 sums (their order fixed by the
+        // inputs) in int64 fixed point, stored, or added exactly when the
+        // band is split over items; det_cast_kernel rounds them afterwards.
+        const long long q0 = to_fixed(v0, det_s), q1 = to_fixed(v1, det_s);
+        if (!several) {
+          __builtin_amdgcn_raw_buffer_store_b128(
+              i32x4{(int)(uint32_t)q0, (int)(q0 >> 32), (int)(uint32_t)q1, (int)(q1 >> 32)}, rc,
+              el * 8u, 0, 0);
+        } else {
+          if (q0 != 0) raw_buffer_atomic_add_i64(q0, rc, (int)(el * 8u), 0, 0);
+          if (q1 != 0) raw_buffer_atomic_add_i64(q1, rc, (int)(el * 8u + 8u), 0, 0);
+        }
+      } else if (!several) {
         if constexpr (A::kBytes == 4) {
           __builtin_amdgcn_raw_buffer_store_b64(i32x2{__float_as_int(v0), __float_as_int(v1)}, rc,
                                                 el * 4u, 0, 0);
@@ -638,17 +794,19 @@ hipError_t launch_acc(int rb, const Params& p, const BinArgs& a, hipStream_t st)
 }
 
 template <class T, bool FUSED>
-hipError_t launch_t(bool f32acc, const Params& p, const BinArgs& a, hipStream_t st) {
+hipError_t launch_t(bool f32acc, bool det, const Params& p, const BinArgs& a, hipStream_t st) {
   const int ng = a.ngroups;
-  hipError_t e = launch_zero(a.counts, (uint64_t)ng * a.nbmax * 4u, st);
-  if (e != hipSuccess) return e;
   const dim3 gbin((unsigned)(ng * a.nqb));
-  hipLaunchKernelGGL((bin_kernel<T, FUSED, false>), gbin, dim3(kBlock), 0, st, p, a);
+  hipLaunchKernelGGL((bin_count_kernel<T, FUSED>), gbin, dim3(kBlock), 0, st, p, a);
   hipLaunchKernelGGL(bin_scan_kernel, dim3((unsigned)ng), dim3(kBlock), 0, st, p, a);
-  hipLaunchKernelGGL((bin_kernel<T, FUSED, true>), gbin, dim3(kBlock), 0, st, p, a);
-  e = hipGetLastError();
+  hipLaunchKernelGGL((bin_fill_kernel<T, FUSED>), gbin, dim3(kBlock), 0, st, p, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // The count matrix lived in the accumulator; now it is zeroed for the sums.
+  e = launch_zero(p.grad_acc, p.acc_bytes, st);
   if (e != hipSuccess) return e;
   const int rb = p.D * T::kBytes;
+  if (det) return launch_acc<T, I64, FUSED>(rb, p, a, st);
   if constexpr (T::kBytes == 4) {
     (void)f32acc;
     return launch_acc<T, F32, FUSED>(rb, p, a, st);
@@ -660,7 +818,8 @@ hipError_t launch_t(bool f32acc, const Params& p, const BinArgs& a, hipStream_t 
 }  // namespace
 
 bool bin_plan(int64_t B, int64_t Q, int64_t M, int64_t K, int64_t D, int64_t S, int64_t L,
-              int elem_bytes, void* grad_loc, void* grad_attn, BinArgs* a) {
+              int elem_bytes, void* grad_loc, void* grad_attn, void* acc, int acc_elem_bytes,
+              BinArgs* a) {
   const int64_t rb = D * elem_bytes;
   if (rb != 32 && rb != 64 && rb != 128) return false;
   if (D > kWave || (D & (D - 1)) != 0) return false;
@@ -681,26 +840,32 @@ bool bin_plan(int64_t B, int64_t Q, int64_t M, int64_t K, int64_t D, int64_t S, 
   const int64_t cap = bands + (2 * qk + kBinChunk - 1) / kBinChunk + 16;
   // Entries: 4 bytes per sample in grad_loc (2 * elem_bytes per sample).
   if ((reinterpret_cast<uintptr_t>(grad_loc) & 3u) != 0) return false;
-  // Counts, cursors, item counts, then 16-byte aligned items in grad_attn.
+  // Cursors, item counts, the item counter, then 16-byte aligned items in
+  // grad_attn.
   uintptr_t base = reinterpret_cast<uintptr_t>(grad_attn);
   if ((base & 3u) != 0) return false;
   const uint64_t avail = (uint64_t)(ng * qk * elem_bytes);
-  const uint64_t n_cnt = (uint64_t)(ng * nbmax) * 4u;
-  uint64_t off_items = 2 * n_cnt + (uint64_t)ng * 4u + 4u;  // + the item counter
+  const uint64_t n_cur = (uint64_t)(ng * nbmax) * 4u;
+  uint64_t off_items = n_cur + (uint64_t)ng * 4u + 4u * kBinXcds;
   off_items += (16u - ((base + off_items) & 15u)) & 15u;
   const uint64_t need = off_items + (uint64_t)(ng * cap) * 16u;
   if (need > avail || (uint64_t)(ng * qk * 2 * elem_bytes) > 0xffffffffull) return false;
+  // The count matrix (one row of keys per sample block) in the accumulator,
+  // which is zeroed after the binning.
+  const int64_t nqb = (qk + kBinPerWg - 1) / kBinPerWg;
+  if ((reinterpret_cast<uintptr_t>(acc) & 3u) != 0) return false;
+  if ((uint64_t)(ng * nqb * nbmax) * 4u > (uint64_t)(B * S * M * D * acc_elem_bytes)) return false;
   char* ws = static_cast<char*>(grad_attn);
   a->entries = static_cast<uint32_t*>(grad_loc);
-  a->counts = reinterpret_cast<uint32_t*>(ws);
-  a->cursors = reinterpret_cast<uint32_t*>(ws + n_cnt);
-  a->nitems = reinterpret_cast<uint32_t*>(ws + 2 * n_cnt);
-  a->next = reinterpret_cast<uint32_t*>(ws + 2 * n_cnt + (uint64_t)ng * 4u);
+  a->cursors = reinterpret_cast<uint32_t*>(ws);
+  a->nitems = reinterpret_cast<uint32_t*>(ws + n_cur);
+  a->next = reinterpret_cast<uint32_t*>(ws + n_cur + (uint64_t)ng * 4u);
   a->items = reinterpret_cast<uint4*>(ws + off_items);
+  a->mat = static_cast<uint32_t*>(acc);
   a->ngroups = (int32_t)ng;
   a->nbmax = (int32_t)nbmax;
   a->cap = (int32_t)cap;
-  a->nqb = (int32_t)((qk + kBinPerWg - 1) / kBinPerWg);
+  a->nqb = (int32_t)nqb;
   a->log2p = log2p;
   a->log2k = log2k;
   a->chunk = kBinChunk;
@@ -709,14 +874,19 @@ bool bin_plan(int64_t B, int64_t Q, int64_t M, int64_t K, int64_t D, int64_t S, 
   return true;
 }
 
-hipError_t launch_binned(int dtype, bool fused, bool f32acc, const Params& p, const BinArgs& a,
-                         hipStream_t st) {
+hipError_t launch_binned(int dtype, bool fused, bool f32acc, bool det, const Params& p,
+                         const BinArgs& a, hipStream_t st) {
   if (a.ngroups <= 0) return hipSuccess;
   switch (dtype) {
-    case kF32: return fused ? launch_t<F32, true>(false, p, a, st) : launch_t<F32, false>(false, p, a, st);
-    case kF16: return fused ? launch_t<F16, true>(f32acc, p, a, st) : launch_t<F16, false>(f32acc, p, a, st);
+    case kF32:
+      return fused ? launch_t<F32, true>(false, det, p, a, st)
+                   : launch_t<F32, false>(false, det, p, a, st);
+    case kF16:
+      return fused ? launch_t<F16, true>(f32acc, det, p, a, st)
+                   : launch_t<F16, false>(f32acc, det, p, a, st);
     case kBF16:
-      return fused ? launch_t<BF16, true>(f32acc, p, a, st) : launch_t<BF16, false>(f32acc, p, a, st);
+      return fused ? launch_t<BF16, true>(f32acc, det, p, a, st)
+                   : launch_t<BF16, false>(f32acc, det, p, a, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -147,12 +147,12 @@ static char* at(void* base, int64_t elems, int e) { return static_cast<char*>(ba
 
 // Binned owner path: batch slices of at most kBinMaxGroups (b, m, level)
 // groups, each within the 32-bit slice limits, whose grad_loc / grad_attn
-// hold the slice's bookkeeping (bin_plan).  On success *bs_out is the slice
-// size.  grad_loc == NULL (msda_backward_plan): buffers at 256-byte aligned
-// addresses are assumed, so the alignment padding is the one a torch
-// allocation would see.
-static bool binned_slices(const Dims& d, int e, void* grad_loc, void* grad_attn,
-                          int64_t* bs_out) {
+// and accumulator (acc, acc_e bytes per element) hold the slice's
+// bookkeeping (bin_plan).  On success *bs_out is the slice size.  NULL
+// buffers (msda_backward_plan): buffers at 256-byte aligned addresses are
+// assumed, so the alignment padding is the one a torch allocation would see.
+static bool binned_slices(const Dims& d, int e, void* grad_loc, void* grad_attn, void* acc,
+                          int acc_e, int64_t* bs_out) {
   const int64_t per_b = d.M * d.L;
   int64_t bs = slice_batch(d);
   if (per_b <= 0 || per_b > kBinMaxGroups || bs <= 0) return false;
@@ -163,8 +163,10 @@ static bool binned_slices(const Dims& d, int e, void* grad_loc, void* grad_attn,
     void* gl = grad_loc ? at(grad_loc, so * 2, e)
                         : reinterpret_cast<void*>((uintptr_t)(so * 2 * e));
     void* ga = grad_attn ? at(grad_attn, so, e) : reinterpret_cast<void*>((uintptr_t)(so * e));
+    const int64_t vo = b0 * d.S * d.M * d.D;
+    void* ac = acc ? at(acc, vo, acc_e) : reinterpret_cast<void*>((uintptr_t)(vo * acc_e));
     BinArgs ba;
-    if (!bin_plan(nb, d.Q, d.M, d.K, d.D, d.S, d.L, e, gl, ga, &ba)) return false;
+    if (!bin_plan(nb, d.Q, d.M, d.K, d.D, d.S, d.L, e, gl, ga, ac, acc_e, &ba)) return false;
   }
   *bs_out = bs;
   return true;
@@ -282,16 +284,23 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
   // Binned owner path (many samples per (b, m, level)): every slice's
   // grad_loc / grad_attn must hold its bookkeeping (bin_plan).
   int64_t bs_bin = 0;
-  const bool binned = compute && !owner && !deterministic && bwd_bin_enabled() &&
-                      binned_slices(d, e, grad_loc, grad_attn, &bs_bin);
+  const bool binned =
+      compute && !owner && bwd_bin_enabled() &&
+      binned_slices(d, e, grad_loc, grad_attn,
+                    det ? det_workspace
+                        : fp32_acc ? static_cast<void*>(grad_value_accum) : grad_value,
+                    det ? 8 : fp32_acc ? 4 : e, &bs_bin);
   const AccMode mode = det ? kAccI64 : fp32_acc ? kAccF32 : kAccNative;
   void* acc = det ? det_workspace : fp32_acc ? static_cast<void*>(grad_value_accum) : grad_value;
   const int acc_e = det ? 8 : fp32_acc ? 4 : e;
   uint32_t* det_max =
       det ? reinterpret_cast<uint32_t*>(static_cast<char*>(det_workspace) + n_val * 8) : nullptr;
 
-  if (!owner) {
+  if (!owner && !binned) {  // the binned path zeroes its accumulator after binning
     rc = status(launch_zero(acc, (uint64_t)(n_val * acc_e) + (det ? 8u : 0u), st));
+    if (rc != MSDA_OK) return rc;
+  } else if (det) {  // binned: only the two max words start at zero here
+    rc = status(launch_zero(det_max, 8u, st));
     if (rc != MSDA_OK) return rc;
   }
   if (det && compute) {
@@ -362,11 +371,12 @@ static int backward_impl(const void* value, const int64_t* spatial_shapes,
       }
       if (binned) {
         BinArgs ba;
-        if (!bin_plan(nb, d.Q, d.M, d.K, d.D, d.S, d.L, e, p.grad_loc, p.grad_attn, &ba))
+        if (!bin_plan(nb, d.Q, d.M, d.K, d.D, d.S, d.L, e, p.grad_loc, p.grad_attn, p.grad_acc,
+                      acc_e, &ba))
           return MSDA_ERR_LAUNCH;  // checked for every slice above
         if (f) p.ref_bytes = (uint32_t)(nb * ref_per_b * e);
         finish_params(sh, kBwdRecords, &p);
-        rc = status(launch_binned(dtype, f != nullptr, fp32_acc, p, ba, st));
+        rc = status(launch_binned(dtype, f != nullptr, fp32_acc, det, p, ba, st));
         // grad_loc / grad_attn (their bookkeeping contents overwritten).
         if (rc == MSDA_OK) rc = status(launch_backward(dtype, kAccNone, f != nullptr, sh, p, st));
         if (rc != MSDA_OK) return rc;
@@ -812,8 +822,8 @@ extern "C" int msda_backward_plan(int64_t batch, int64_t num_keys, int64_t num_h
   if (compute && bwd_owner_enabled() && owner_plan(d.B, d.Q, d.K, d.D, d.S, d.L, e, &own))
     return MSDA_BACKWARD_OWNER;
   int64_t bs_bin = 0;
-  if (compute && !deterministic && bwd_bin_enabled() &&
-      binned_slices(d, e, nullptr, nullptr, &bs_bin))
+  if (compute && bwd_bin_enabled() &&
+      binned_slices(d, e, nullptr, nullptr, nullptr, deterministic ? 8 : e, &bs_bin))
     return MSDA_BACKWARD_BINNED;
   Shape sh;
   if (compute && !choose_shape((int)(d.D * e), (int)(d.L * d.K), d.B * d.Q * d.M, true,

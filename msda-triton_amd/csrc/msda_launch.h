@@ -73,23 +73,30 @@ constexpr int kBinMaxBands = 4096;   // bands per level
 constexpr int kBinMaxGroups = 1024;  // (b, m, level) groups per launch
 constexpr int kBinChunk = 4096;      // entries per work item (at most, unless items run short)
 struct BinArgs {
-  uint32_t* entries;  // [group][Q*K] sample ids q*K + k, by band (in grad_loc)
-  uint32_t* counts;   // [group][nbmax] samples keyed to each key (2^log2k pixels)
-  uint32_t* cursors;  // [group][nbmax] first entry of each key, then fill cursor
+  uint32_t* entries;  // [group][Q*K] sample ids q*K + k, by key (in grad_loc)
+  uint32_t* mat;      // [group][nqb][nbmax] per sample block: its samples per key,
+                      // then their first slot within the key (in the accumulator)
+  uint32_t* cursors;  // [group][nbmax] first entry of each key
   uint32_t* nitems;   // [group] work items
-  uint32_t* next;     // work-item counter of bin_acc_kernel (zeroed by bin_scan_kernel)
+  uint32_t* next;     // [8] work-item counters of bin_acc_kernel, one per XCD (zeroed by
+                      // bin_scan_kernel)
   uint4* items;       // [group][cap] (band | split << 31, first entry, end entry, 0)
   uint32_t loc_bytes, attn_bytes;
   int32_t ngroups, nbmax, cap, nqb, log2p, log2k, chunk;  // bands of 2^log2p pixels
 };
 // Fills `a` for a slice of B batches; false when the shapes or the buffers
-// (size, alignment) do not suit the path.  NULL buffers: shape check only.
+// (size, alignment) do not suit the path.  `acc` (B*S*M*D elements of
+// acc_elem_bytes: grad_value or the fp32 scratch) holds the count matrix
+// during the binning.
 bool bin_plan(int64_t B, int64_t Q, int64_t M, int64_t K, int64_t D, int64_t S, int64_t L,
-              int elem_bytes, void* grad_loc, void* grad_attn, BinArgs* a);
-// Zeroes the counts and runs the four kernels; grad_value (p.grad_acc, of
-// element type fp32 when f32acc or dtype is fp32) must be zero on entry.
-hipError_t launch_binned(int dtype, bool fused, bool f32acc, const Params& p, const BinArgs& a,
-                         hipStream_t st);
+              int elem_bytes, void* grad_loc, void* grad_attn, void* acc, int acc_elem_bytes,
+              BinArgs* a);
+// Bins the samples, zeroes p.grad_acc (the accumulator: grad_value, or the
+// fp32 scratch when f32acc, fp32 for fp32 dtype; det: the int64 fixed-point
+// accumulator of the deterministic backward, scale from p.det_max) and sums
+// the bands into it.
+hipError_t launch_binned(int dtype, bool fused, bool f32acc, bool det, const Params& p,
+                         const BinArgs& a, hipStream_t st);
 // Fused front-end: reference-point gradient from the offset gradients, one
 // wave per (b, q) of the nbq in the call.
 hipError_t launch_ref_grad(int dtype, const Params& p, uint64_t nbq, hipStream_t st);

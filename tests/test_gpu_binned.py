@@ -141,3 +141,42 @@ def test_fused_binned_split_bands(dtype, per_level):
     out, g, grads = run_fused(value, sh, starts, ref, off, logits)
     ref_out, ref_grads = run_fused_reference(value, sh, ref, off, logits, g)
     check_fused(out, grads, ref_out, ref_grads, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("case", BIN_CASES[:3], ids=[c["id"] for c in BIN_CASES[:3]])
+def test_deterministic_binned_matches_reference(case, dtype):
+    """deterministic=True on the binned path (int64 fixed-point band sums):
+    identical bits on two calls, oracle parity."""
+    value, shapes, starts, loc, attn = _inputs(case, dtype, loc_lo=-0.1, loc_hi=1.1)
+    if value.dtype == torch.float32 and case["D"] == 64:
+        pytest.skip("256-byte fp32 rows: not on the binned path")
+    B, S, M, D = value.shape
+    _, Q, _, L, K, _ = loc.shape
+    from msda_triton_amd import _native
+    code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dtype]
+    assert _native.load().msda_backward_plan(B, S, M, D, Q, L, K, code, 1) == BINNED
+    g1, grads1 = fwd_bwd(value, shapes, starts, loc, attn, deterministic=True)
+    g2, grads2 = fwd_bwd(value, shapes, starts, loc, attn, deterministic=True)
+    for a, b in zip(grads1, grads2):
+        assert torch.equal(a, b)
+    _, refs = reference_grads(value, shapes, loc, attn, g1)
+    check_grads(grads1, refs, dtype, shapes)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_deterministic_binned_split_bands(dtype):
+    """Split bands (several work items per band) in deterministic mode: the
+    items' int64 partial sums add exactly, so two calls agree bit for bit."""
+    B, Q, M, D, K = 1, 1500, 2, 32, 4
+    shapes = [(40, 60), (20, 30)]
+    value, sh, starts, loc, attn = make_inputs(B=B, Q=Q, M=M, D=D, shapes=shapes, K=K,
+                                               dtype=dtype, device=DEVICE)
+    gen = torch.Generator().manual_seed(5)
+    loc = (0.5 + 0.01 * torch.randn(loc.shape, generator=gen)).to(DEVICE, dtype)
+    g1, grads1 = fwd_bwd(value, sh, starts, loc, attn, deterministic=True)
+    g2, grads2 = fwd_bwd(value, sh, starts, loc, attn, deterministic=True)
+    for a, b in zip(grads1, grads2):
+        assert torch.equal(a, b)
+    _, refs = reference_grads(value, sh, loc, attn, g1)
+    check_grads(grads1, refs, dtype, sh)

@@ -21,11 +21,11 @@ pytestmark = pytest.mark.gpu
 DEVICE = "cuda"
 
 
-def _fwd_bwd(name, fp32_grad_accum):
+def _fwd_bwd(name, fp32_grad_accum, **kw):
     value, shapes, starts, loc, attn = presets.make_preset_inputs(name, device=DEVICE)
     g = presets.make_grad_out(name, device=DEVICE)
     v, lo, a = (t.clone().requires_grad_(True) for t in (value, loc, attn))
-    out = msda(v, shapes, starts, lo, a, fp32_grad_accum=fp32_grad_accum)
+    out = msda(v, shapes, starts, lo, a, fp32_grad_accum=fp32_grad_accum, **kw)
     out.backward(g)
     torch.cuda.synchronize()
     return (value, shapes, loc, attn, g), out.detach(), (v.grad, lo.grad, a.grad)
@@ -63,6 +63,29 @@ def test_preset_matches_oracle(name, fp32_grad_accum):
         if nm == "grad_loc" and dtype == torch.float32:  # elementwise per pixel (per_pixel)
             x, r = per_pixel(x, shapes).float(), per_pixel(r, shapes).float()
         torch.testing.assert_close(x.float().cpu(), r, **BWD_TOL[dtype], msg=lambda m: f"{nm}: {m}")
+
+
+@pytest.mark.parametrize("name", ["encoder", "mask2former_fp32", "mask2former_bf16"])
+def test_deterministic_binned_preset(name):
+    """The deterministic backward of the encoder-style presets takes the
+    binned path (int64 fixed-point band sums): two calls give identical bits,
+    and the result matches the float64 oracle."""
+    from msda_triton_amd import _native
+
+    c = presets.preset_dims(name)
+    dtype = presets.PRESETS[name]["dtype"]
+    code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dtype]
+    plan = _native.load().msda_backward_plan(c["B"], c["S"], c["M"], c["D"], c["Q"], c["L"],
+                                             c["K"], code, 1)
+    assert plan == 3  # MSDA_BACKWARD_BINNED
+    (value, shapes, loc, attn, g), _, grads1 = _fwd_bwd(name, False, deterministic=True)
+    _, _, grads2 = _fwd_bwd(name, False, deterministic=True)
+    for x, y in zip(grads1, grads2):
+        assert torch.equal(x, y)
+    _, refs = run_reference(value, shapes, loc, attn, g, dtype=torch.float64)
+    for nm, x, r in zip(("grad_value", "grad_loc", "grad_attn"), grads1, refs):
+        e = rel_err(x, r)
+        assert e <= BWD_RELERR[dtype], f"{name} {nm}: rel_err {e:.3e}"
 
 
 @pytest.mark.parametrize("name", ["decoder", "encoder", "mask2former_fp32"])

@@ -216,7 +216,7 @@ def test_backward_plan(lib, overrides):
     # decoder (B4 Q300 L4 K4, bf16): Q*K = 1200 per level, 64-byte rows
     assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 0) == owner
     assert lib.msda_backward_plan(4, 22223, 8, 32, 300, 4, 4, 2, 1) == owner  # deterministic
-    assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 1) == dedup
+    assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 1) == binned  # deterministic
     # encoder / Mask2Former: Q = S, far more samples per (b, m, level)
     assert lib.msda_backward_plan(2, 22223, 8, 32, 22223, 4, 4, 1, 0) == binned
     assert lib.msda_backward_plan(2, 21504, 8, 32, 21504, 3, 4, 0, 0) == binned
