@@ -31,8 +31,10 @@
  *   - Arithmetic is fp32 for every storage dtype; results are rounded once to
  *     the storage dtype.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream).
- *     No entry point synchronises, allocates device memory or keeps state
- *     between calls; all of them may be captured into a hipGraph.
+ *     No entry point synchronises or allocates device memory, and none
+ *     keeps state between calls apart from the launch overrides set by
+ *     msda_set_launch_override (unset by default); all of them may be
+ *     captured into a hipGraph.
  *   - The return value is MSDA_OK or one of the MSDA_ERR_* codes below; the
  *     device buffers are untouched when an argument error is returned.
  */
@@ -98,18 +100,19 @@ int msda_forward(const void* value, const int64_t* spatial_shapes,
  * Q*D*elem <= 40960, 16-byte aligned grad_output and grad_value -- workgroups
  * that own bands of value rows sum each element's contributions in fp32 and
  * store it once (no atomics, no zero-fill, grad_value_accum unused);
- * otherwise grad_value is zero-filled on `stream` and, for head rows of 32,
- * 64 or 128 bytes with D a power of two, the samples are binned by band of
- * value rows (the bins kept in grad_sampling_locations and
- * grad_attention_weights before those are written) and each band's rows are
- * summed in fp32 by one workgroup, which stores them, or by several, which
- * add them with atomics; for other shapes the atomics are issued by a
- * kernel that merges samples sharing a row within a workgroup or by the
- * direct scatter.  On the owner
+ * otherwise, for head rows of 32, 64 or 128 bytes with D a power of two,
+ * the samples are binned by band of value rows (the bins kept in
+ * grad_sampling_locations and grad_attention_weights before those are
+ * written, a count matrix in the accumulator -- grad_value or
+ * grad_value_accum -- before it is zero-filled on `stream`) and each band's
+ * rows are summed in fp32 by one workgroup, which stores them, or by
+ * several, which add them with atomics; for other shapes grad_value is
+ * zero-filled and the atomics are issued by a kernel that merges samples
+ * sharing a row within a workgroup or by the direct scatter.  On the owner
  * path grad_value is bitwise reproducible (each element one fp32 sum in an
- * order fixed by the inputs); on the binned and atomic paths it is not (the order of
- * the atomics varies).  The other two gradients are reproducible on every
- * path.
+ * order fixed by the inputs); on the binned path wherever no band is split
+ * over workgroups; on the atomic paths it is not (the order of the atomics
+ * varies).  The other two gradients are reproducible on every path.
  */
 int msda_backward(const void* value, const int64_t* spatial_shapes,
                   const int64_t* level_start_index, const void* sampling_locations,
@@ -183,9 +186,11 @@ int msda_fused_backward(const void* value, const int64_t* spatial_shapes,
  * path (msda_backward_plan(..., 1) == MSDA_BACKWARD_OWNER; see msda_backward)
  * get it from there: every element is one fp32 sum over its contributions
  * in an order fixed by the inputs, no workspace needed.  Other calls
- * accumulate in int64 fixed point: each contribution c is added as
- * round(c * 2^e), integer addition is exact, and the result does not depend
- * on the order.  e is chosen per call from Q*L*K * max|A| *
+ * accumulate in int64 fixed point: on the binned path
+ * (MSDA_BACKWARD_BINNED) each band's fp32 sums, formed in an order fixed by
+ * the inputs, enter as round(sum * 2^e); on the atomic paths each
+ * contribution c does, as round(c * 2^e); integer addition is exact, and
+ * the result does not depend on the order.  e is chosen per call from Q*L*K * max|A| *
  * max|grad_output| (a bound on every element) so that no sum can overflow;
  * the resolution, that bound times 2^-60, is far below fp32 rounding.
  * grad_sampling_locations / grad_attention_weights (and the fused
@@ -196,7 +201,9 @@ int msda_fused_backward(const void* value, const int64_t* spatial_shapes,
  *               words; 0 when the call takes the owner path, given 16-byte
  *               aligned grad_output and grad_value -- workspace may then be
  *               NULL; -1 for invalid sizes or dtype); its contents on entry
- *               do not matter.
+ *               do not matter.  With a misaligned grad_output the owner path
+ *               is ruled out: pass the full B*S*M*D*8 + 64 bytes, or the
+ *               call returns MSDA_ERR_INVALID_ARGUMENT before any launch.
  * Other arguments as in msda_backward / msda_fused_backward (no fp32
  * accumulator: the integer accumulator replaces it).
  */
@@ -309,10 +316,12 @@ int msda_abi_version(void);
 /*
  * Which way msda_backward / msda_fused_backward (deterministic == 0) or their
  * deterministic variants (deterministic != 0) form grad_value for these
- * sizes, assuming 16-byte aligned grad_output and grad_value: one of the
- * MSDA_BACKWARD_* codes below, or minus an MSDA_ERR_* code for sizes or a
- * dtype the backward rejects.  Host-only (no device work); it reads the
- * same MSDA_BWD_OWNER / MSDA_BWD_PRIV overrides as the backward.  No
+ * sizes, assuming 16-byte aligned grad_output and grad_value (and, for the
+ * binned path's bookkeeping, 256-byte aligned buffers, as torch allocates):
+ * one of the MSDA_BACKWARD_* codes below, or minus an MSDA_ERR_* code for
+ * sizes or a dtype the backward rejects.  Host-only (no device work); it
+ * follows the same launch overrides (msda_set_launch_override) as the
+ * backward.  No
  * counterpart in the reference, whose backward has a single kernel
  * (src/msda_triton/ops.py:76-92): it serves callers and benchmarks that
  * report which kernels ran.
@@ -320,8 +329,8 @@ int msda_abi_version(void);
 #define MSDA_BACKWARD_ATOMIC_DIRECT 0 /* zero-fill + direct atomic scatter */
 #define MSDA_BACKWARD_ATOMIC_DEDUP 1  /* zero-fill + row-merging atomic kernel */
 #define MSDA_BACKWARD_OWNER 2         /* row-owner kernel + scatter-free gradient kernel */
-#define MSDA_BACKWARD_BINNED 3        /* zero-fill + samples binned by band of value rows,
-                                         band sums in LDS + scatter-free gradient kernel */
+#define MSDA_BACKWARD_BINNED 3        /* samples binned by band of value rows, zero-fill,
+                                         band sums + scatter-free gradient kernel */
 int msda_backward_plan(int64_t batch, int64_t num_keys, int64_t num_heads, int64_t head_dim,
                        int64_t num_queries, int64_t num_levels, int64_t num_points, int dtype,
                        int deterministic);
