@@ -108,20 +108,42 @@ __device__ int own_band(const Params& p, int gi, int& lo, int& hi, int& lv, OwnL
   return lo < hi ? 2 : 0;
 }
 
-// Exclusive prefix sum over the workgroup; `tot` receives the total.
-__device__ __forceinline__ int own_scan(int v, int* wsum, int* tot) {
+// Maximum of v over the wave (every lane active): DPP within each row of 16
+// lanes (swap neighbours, pairs, mirror the halves, mirror the row), then
+// the four rows' maxima read as scalars.
+__device__ __forceinline__ int own_wave_max(int v) {
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false));  // row_mirror
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// Exclusive prefix sum of v over the workgroup; `tot` receives the total
+// and `mx` the maximum of m.
+__device__ __forceinline__ int own_scan(int v, int m, int* wsum, int* wmax, int* tot, int* mx) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int wm = own_wave_max(m);
   int x = v;
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
     const int y = __shfl_up(x, d);
     if (lane >= d) x += y;
   }
-  if (lane == kWave - 1) wsum[wave] = x;
+  if (lane == kWave - 1) {
+    // The addresses are formed here: hoisted to the kernel's start they
+    // would hold a register throughout (and be spilled).
+    int w = wave;
+    asm volatile("" : "+v"(w));
+    wsum[w] = x;
+    wmax[w] = wm;
+  }
   __syncthreads();
   int base = 0;
   for (int w = 0; w < wave; ++w) base += wsum[w];
   *tot = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  *mx = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
   return base + x - v;
 }
 
@@ -529,12 +551,13 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
     __syncthreads();
 
     // 2. CSR offsets of the rows' totals; each wave's counter becomes the
-    // sum over the waves before it.
+    // sum over the waves before it.  maxlen: the longest row's entries.
+    int maxlen;
     {
       // Row totals < 2^16 (a row takes at most one corner per sample), so
       // two share a word here too.
       uint32_t c2[4];
-      int sum = 0;
+      int sum = 0, mloc = 0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int wd = tid * 4 + k;  // rows 2 wd, 2 wd + 1
@@ -549,9 +572,10 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
         }
         c2[k] = c;
         sum += (int)((c & 0xffffu) + (c >> 16));
+        mloc = max(mloc, (int)max(c & 0xffffu, c >> 16));
       }
       int tot;
-      int ex = own_scan(sum, s_wsum, &tot);
+      int ex = own_scan(sum, mloc, s_wsum, smem.own.s_qc[1], &tot, &maxlen);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int r = tid * 8 + k;
@@ -655,9 +679,14 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
       // of a row that started in an earlier slice waits in `first`, the
       // piece of a row that runs on into later slices in `tail`.
       const int cs = (ne + kTeams - 1) / kTeams;
+      // Pieces are summed in groups of pg (pg^2 >= kTeams - 1: at most pg
+      // groups per row); a row of len entries spans at most pg + 1 slices
+      // when len <= pg * cs.
+      constexpr int kPGMax = 16;
+      const int pg = kTeams > 64 ? 16 : 8;
       const int e_lo = min(team * cs, ne), e_hi = min(e_lo + cs, ne);
       float first[kVec], acc[kVec];
-      bool has_first = false;
+      int prow = -1;  // the row of the piece in `first`, if any
       int tail_row = -1;
 #pragma unroll
       for (int k = 0; k < kVec; ++k) first[k] = acc[k] = 0.f;
@@ -693,7 +722,7 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
                 if (cur == row0 && first_part) {
 #pragma unroll
                   for (int v = 0; v < kVec; ++v) first[v] = acc[v];
-                  has_first = true;
+                  prow = row0;
                 } else {
                   put(cur, acc, written);
                 }
@@ -712,25 +741,99 @@ __global__ __launch_bounds__(kBlock, 4) void owner_kernel(Params p, Params pd) {
         if (cur == row0 && first_part) {  // a piece (the slice lies inside one row)
 #pragma unroll
           for (int v = 0; v < kVec; ++v) first[v] = acc[v];
-          has_first = true;
+          prow = row0;
         } else if (s_off[cur + 1] - base > e_hi) {
           tail_row = cur;  // acc stays the tail
         } else {
           put(cur, acc, written);
         }
       }
+      // The pieces of a row that spans slices t1 + 1 .. t2 (t1 holds its
+      // tail) lie in consecutive teams.  The tail team adds them in order
+      // when the row is at most pg slices long (at most pg pieces: the
+      // common case).  A longer (deep) row -- heavy contention: dozens of
+      // slices -- is summed in two steps: the group heads t1 + 1 + j pg add
+      // the pieces of their group of pg, loads in flight together, and the
+      // tail team adds the group sums.  The second step runs when the band's
+      // longest row (maxlen, from the scan) could be deep.  Which step runs,
+      // and every addition, follows from the CSR alone: the sums are the
+      // same on every run.
+      const bool grouped = maxlen > pg * cs;  // some row of the band is deep (uniform)
       __syncthreads();  // every entry read: the pieces may overwrite the CSR
-      if (has_first) {
+      if (prow >= 0) {
 #pragma unroll
         for (int k = 0; k < kVec; ++k) u.piece[(team * G + ch) * kVec + k] = first[k];
       }
       __syncthreads();
-      if (tail_row >= 0) {  // add the pieces of the later slices, in order
-        const int t2 = (s_off[tail_row + 1] - base - 1) / cs;
-#pragma unroll 4
-        for (int t = team + 1; t <= t2; ++t) {
+      if (grouped) {
+        // Group heads t1 + 1 + j pg of the deep rows: the group's sum
+        // replaces the head's piece (no other team reads that slot).
+        const int p0 = prow >= 0 ? s_off[prow] - base : 0;
+        const int p1 = prow >= 0 ? s_off[prow + 1] - base : 0;
+        if (p1 - p0 > pg * cs) {  // a piece of a deep row
+          const int t1 = p0 / cs, t2 = (p1 - 1) / cs;
+          if (((team - t1 - 1) & (pg - 1)) == 0) {
+            const int n = min(pg, t2 - team + 1);
+            int th = team;  // addresses formed here (not hoisted: registers)
+            asm volatile("" : "+v"(th));
 #pragma unroll
-          for (int k = 0; k < kVec; ++k) acc[k] += u.piece[(t * G + ch) * kVec + k];
+            for (int j = 1; j < kPGMax; j += 4) {
+              if (j >= n) break;
+              float pc[4][kVec];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int t = th + min(j + i, n - 1);
+#pragma unroll
+                for (int k = 0; k < kVec; ++k) pc[i][k] = u.piece[(t * G + ch) * kVec + k];
+              }
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                if (j + i < n) {
+#pragma unroll
+                  for (int k = 0; k < kVec; ++k) first[k] += pc[i][k];
+                }
+              }
+            }
+#pragma unroll
+            for (int k = 0; k < kVec; ++k) u.piece[(team * G + ch) * kVec + k] = first[k];
+          }
+        }
+        __syncthreads();  // group sums stored
+      }
+      if (tail_row >= 0) {  // the tail, then the later pieces (or group sums) in order
+        const int c0 = s_off[tail_row] - base, c1 = s_off[tail_row + 1] - base;
+        const int te = (c1 - 1) / cs;  // the row's last team
+        if (!grouped) {
+#pragma unroll 4
+          for (int t = team + 1; t <= te; ++t) {
+#pragma unroll
+            for (int k = 0; k < kVec; ++k) acc[k] += u.piece[(t * G + ch) * kVec + k];
+          }
+        } else {
+          const int step = c1 - c0 > pg * cs ? pg : 1;
+          const int cnt = (te - team - 1) / step + 1;  // 1 .. pg slots
+          // Their addresses are formed here, not hoisted to the kernel's
+          // start, where they would hold registers for the whole kernel.
+          int t0 = team + 1;
+          asm volatile("" : "+v"(t0));
+#pragma unroll
+          for (int j = 0; j < kPGMax; j += 4) {
+            if (j >= cnt) break;
+            float pc[4][kVec];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int t = t0 + min(j + i, cnt - 1) * step;
+#pragma unroll
+              for (int k = 0; k < kVec; ++k) pc[i][k] = u.piece[(t * G + ch) * kVec + k];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if (j + i < cnt) {
+#pragma unroll
+                for (int k = 0; k < kVec; ++k) acc[k] += pc[i][k];
+              }
+            }
+          }
         }
         put(tail_row, acc, written);
       }

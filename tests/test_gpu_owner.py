@@ -126,12 +126,17 @@ def test_sample_count_boundary(QK):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
-def test_samples_piled_on_one_band(dtype):
+@pytest.mark.parametrize("D", [8, 32])
+def test_samples_piled_on_one_band(dtype, D):
     """All 2048 samples of a (b, m, level) within a pixel or two: 8192 corner
     entries on a handful of rows of one band, more than one CSR pass holds,
-    so the band is processed in several sub-bands."""
+    so the band is processed in several sub-bands, and single rows span
+    dozens of the entry slices (their pieces summed in groups).  D = 8 gives
+    rows of one or two lanes (256 or 128 slices per pass), D = 32 of four
+    or eight.  The sums' order is fixed by the inputs: two runs agree
+    bitwise."""
     value, shapes, starts, loc, attn = make_inputs(
-        B=1, Q=128, M=2, D=32, shapes=[(16, 16), (8, 8)], K=16, dtype=torch.float32,
+        B=1, Q=128, M=2, D=D, shapes=[(16, 16), (8, 8)], K=16, dtype=torch.float32,
         device="cpu")
     gen = torch.Generator().manual_seed(11)
     loc = 0.5 + 0.02 * torch.rand(loc.shape, generator=gen)
@@ -141,6 +146,8 @@ def test_samples_piled_on_one_band(dtype):
     g, grads = fwd_bwd(value, shapes, starts.to(DEVICE), loc, attn)
     _, refs = reference_grads(value, shapes, loc, attn, g)
     check_grads(grads, refs, dtype, shapes)
+    _, again = fwd_bwd(value, shapes, starts.to(DEVICE), loc, attn)
+    assert torch.equal(grads[0], again[0])
 
 
 def _analytic(value, shapes, starts, loc, attn, g):
