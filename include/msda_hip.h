@@ -272,7 +272,12 @@ int64_t msda_projection_workspace_bytes(int64_t rows, int64_t in_features, int64
  *   grad_bias    = column sums of grad_output over unmasked rows, grad_bias2 likewise
  * Weight / bias gradients need `workspace` (msda_projection_workspace_bytes,
  * 16-byte aligned, contents ignored); they are fixed-order sums (no atomics),
- * so every output is bitwise reproducible.
+ * so every output is bitwise reproducible.  When grad_input and a weight or
+ * bias gradient are both asked for, the weight/bias half runs on a second
+ * stream of the library's (one per device, default priority, created on the
+ * first such call), forked from and joined back into `stream` with events:
+ * the call stays ordered on `stream` as a whole (and captures into a HIP
+ * graph as two parallel branches).
  */
 int msda_projection_backward(const void* input, const void* weight, const void* weight2,
                              const uint8_t* row_mask, const void* grad_output,
@@ -292,7 +297,8 @@ int msda_projection_backward(const void* input, const void* weight, const void* 
  * MSDA_ERR_UNSUPPORTED_SHAPE.  Every call on one GPU uses that GPU's one
  * array: calls that overlap on one GPU (other streams, other threads) race
  * and give wrong results -- serialise them.  Arguments and results as in
- * msda_projection_backward (bitwise the same outputs).
+ * msda_projection_backward (bitwise the same outputs); everything runs on
+ * `stream` (no second stream).
  */
 int msda_projection_backward_noalloc(const void* input, const void* weight, const void* weight2,
                                      const uint8_t* row_mask, const void* grad_output,

@@ -638,13 +638,57 @@ extern "C" int64_t msda_projection_workspace_bytes(int64_t rows, int64_t in_feat
          wgrad_workspace_bytes(rows, (int)out_features, (int)in_features, dtype);
 }
 
-extern "C" int msda_projection_backward(const void* input, const void* weight,
-                                        const void* weight2, const uint8_t* row_mask,
-                                        const void* grad_output, const void* grad_output2,
-                                        void* grad_input, void* grad_weight, void* grad_bias,
-                                        void* grad_weight2, void* grad_bias2, void* workspace,
-                                        int64_t rows, int64_t in_features, int64_t out_features,
-                                        int64_t split, int dtype, void* stream) {
+// A second stream per device for the projection backward: the weight
+// gradient (partials + fixed-order reduction) does not depend on grad_input,
+// so it runs beside the transpose and the grad_input launch, forked from and
+// joined back into the caller's stream with events (also under graph
+// capture, where the two become parallel branches).  Default priority,
+// non-blocking; created on a device's first such call made outside graph
+// capture, and kept until the process ends.  The mutex covers the fork/join enqueue, so concurrent
+// callers on one device share the stream without mixing their events.
+constexpr int kSideMaxDevices = 64;
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+static SideStream g_side[kSideMaxDevices];
+static std::mutex g_side_mu;
+
+static SideStream* side_stream_locked(hipStream_t caller) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kSideMaxDevices) return nullptr;
+  SideStream& ss = g_side[dev];
+  if (!ss.s) {
+    // Not created under graph capture (creation may be illegal there): a
+    // first call made while capturing runs on the caller's stream alone.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(caller, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return nullptr;
+    hipStream_t s = nullptr;
+    hipEvent_t f = nullptr, j = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+      if (f) (void)hipEventDestroy(f);
+      (void)hipStreamDestroy(s);
+      return nullptr;
+    }
+    ss.fork = f;
+    ss.join = j;
+    ss.s = s;
+  }
+  return &ss;
+}
+
+// overlap: run the weight gradient on the side stream (msda_projection_backward);
+// the allocation-free entry point runs everything on the caller's stream.
+static int projection_backward_impl(const void* input, const void* weight, const void* weight2,
+                                    const uint8_t* row_mask, const void* grad_output,
+                                    const void* grad_output2, void* grad_input, void* grad_weight,
+                                    void* grad_bias, void* grad_weight2, void* grad_bias2,
+                                    void* workspace, int64_t rows, int64_t in_features,
+                                    int64_t out_features, int64_t split, int dtype, void* stream,
+                                    bool overlap) {
   const ProjDims d{rows, in_features, out_features, split};
   int rc = check_proj(d, dtype);
   if (rc != MSDA_OK) return rc;
@@ -667,11 +711,40 @@ extern "C" int msda_projection_backward(const void* input, const void* weight,
   char* wt = static_cast<char*>(workspace);
   float* partials = reinterpret_cast<float*>(wt + wt_bytes(d, dtype));
 
+  // Weight and bias gradients: on the side stream when both halves run.
+  std::unique_lock<std::mutex> lock(g_side_mu, std::defer_lock);
+  SideStream* side = nullptr;
+  if (overlap && dx && wgrad) {
+    lock.lock();
+    side = side_stream_locked(st);
+    if (side && (hipEventRecord(side->fork, st) != hipSuccess ||
+                 hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess))
+      return MSDA_ERR_LAUNCH;
+  }
+  if (wgrad) {
+    WgradArgs w{};
+    wgrad_plan(rows, (int)out_features, (int)in_features, dtype, &w);
+    w.g0 = grad_output;
+    w.g1 = two ? grad_output2 : nullptr;
+    w.ldg0 = split;
+    w.ldg1 = out_features - split;
+    w.nsplit = (int)split;
+    w.x = input;
+    w.ldx = in_features;
+    w.mask = row_mask;
+    w.ws = partials;
+    w.wsb = (grad_bias || (two && grad_bias2))
+                ? w.ws + (int64_t)w.nchunks * out_features * in_features
+                : nullptr;
+    rc = status(launch_wgrad(dtype, w, grad_weight, two ? grad_weight2 : nullptr, grad_bias,
+                             two ? grad_bias2 : nullptr, side ? side->s : st));
+  }
+
   // grad_input = [g | g2] [W ; W2] = [g | g2] wt^T with wt = [W ; W2]^T
   // (in x out): proj_kernel over the output features as its reduction,
   // segment 0 from grad_output, segment 1 from grad_output2; fp32 splits it
   // into launches of <= 256 that accumulate.
-  if (dx) {
+  if (dx && rc == MSDA_OK) {
     rc = status(launch_transpose(dtype, weight, two ? weight2 : nullptr, (int)split,
                                  (int)out_features, (int)in_features, wt, st));
     const int64_t step = dtype == kF32 ? proj_max_reduction(dtype) : out_features;
@@ -705,24 +778,25 @@ extern "C" int msda_projection_backward(const void* input, const void* weight,
       rc = status(launch_projection(dtype, k0 > 0, a, st));
     }
   }
-  if (rc != MSDA_OK || !wgrad) return rc;
+  if (side) {  // join: the caller's stream waits for the weight gradient
+    if (hipEventRecord(side->join, side->s) != hipSuccess ||
+        hipStreamWaitEvent(st, side->join, 0) != hipSuccess)
+      rc = MSDA_ERR_LAUNCH;
+  }
+  return rc;
+}
 
-  WgradArgs w{};
-  wgrad_plan(rows, (int)out_features, (int)in_features, dtype, &w);
-  w.g0 = grad_output;
-  w.g1 = two ? grad_output2 : nullptr;
-  w.ldg0 = split;
-  w.ldg1 = out_features - split;
-  w.nsplit = (int)split;
-  w.x = input;
-  w.ldx = in_features;
-  w.mask = row_mask;
-  w.ws = partials;
-  w.wsb = (grad_bias || (two && grad_bias2))
-              ? w.ws + (int64_t)w.nchunks * out_features * in_features
-              : nullptr;
-  return status(launch_wgrad(dtype, w, grad_weight, two ? grad_weight2 : nullptr, grad_bias,
-                             two ? grad_bias2 : nullptr, st));
+extern "C" int msda_projection_backward(const void* input, const void* weight,
+                                        const void* weight2, const uint8_t* row_mask,
+                                        const void* grad_output, const void* grad_output2,
+                                        void* grad_input, void* grad_weight, void* grad_bias,
+                                        void* grad_weight2, void* grad_bias2, void* workspace,
+                                        int64_t rows, int64_t in_features, int64_t out_features,
+                                        int64_t split, int dtype, void* stream) {
+  return projection_backward_impl(input, weight, weight2, row_mask, grad_output, grad_output2,
+                                  grad_input, grad_weight, grad_bias, grad_weight2, grad_bias2,
+                                  workspace, rows, in_features, out_features, split, dtype, stream,
+                                  true);
 }
 
 // ---------------------------------------------------------------------------
@@ -778,9 +852,9 @@ extern "C" int msda_projection_backward_noalloc(
     ws = scratch_address();
     if (!ws) return MSDA_ERR_LAUNCH;
   }
-  return msda_projection_backward(input, weight, weight2, row_mask, grad_output, grad_output2,
+  return projection_backward_impl(input, weight, weight2, row_mask, grad_output, grad_output2,
                                   grad_input, grad_weight, grad_bias, grad_weight2, grad_bias2, ws,
-                                  rows, in_features, out_features, split, dtype, stream);
+                                  rows, in_features, out_features, split, dtype, stream, false);
 }
 
 extern "C" const char* msda_error_string(int code) {

@@ -393,8 +393,8 @@ struct Params {
   uint32_t ref_bytes;  //   fused: num_records of the reference points
   int32_t own_mix;     //   order of band and gradient workgroups (0 last, 1 first, 2 after own_est)
   int32_t own_est;     //   bands per (b, m), estimated (host)
-  int32_t own_cut;
-  int32_t own_big;     //   1: the 40 KB grad_out staging build of the kernel     //   band chunks (of 8 workgroups) dispatched before the gradient chunks
+  int32_t own_cut;     //   band chunks (of 8 workgroups) dispatched before the gradient chunks
+  int32_t own_big;     //   1: the 40 KB grad_out staging build of the kernel
   FastDiv div_qm, div_m, div_k, div_d;
 };
 
