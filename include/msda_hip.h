@@ -291,7 +291,7 @@ int msda_projection_backward(const void* input, const void* weight, const void* 
  * nothing.  No counterpart in the reference; it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving or
  * training loops, harnesses that forbid hipMalloc).  The workspace is a
- * device array inside the library, 32 MiB per GPU, held by every GPU the
+ * device array inside the library, 64 MiB per GPU, held by every GPU the
  * library runs on until the process ends; shapes whose workspace
  * (msda_projection_workspace_bytes) exceeds it return
  * MSDA_ERR_UNSUPPORTED_SHAPE.  Every call on one GPU uses that GPU's one

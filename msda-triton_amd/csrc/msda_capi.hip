@@ -806,10 +806,10 @@ extern "C" int msda_projection_backward(const void* input, const void* weight,
 
 // The workspace of msda_projection_backward_noalloc: a file-scope device
 // array, so every GPU the library runs on holds one copy of it from module
-// load until the process ends.  32 MiB covers every half-precision
-// projection the library takes (reductions of at most 512: 17.3 MB at 512 x
+// load until the process ends.  64 MiB covers every half-precision
+// projection the library takes (reductions of at most 512: ~35 MB at 512 x
 // 512 on 256 CUs) and fp32 ones up to 512 x 512.
-constexpr int64_t kNoAllocScratchBytes = (int64_t)32 << 20;
+constexpr int64_t kNoAllocScratchBytes = (int64_t)64 << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 // Device address of `scratch` on each device.  In host code the array's

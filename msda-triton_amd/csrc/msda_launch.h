@@ -157,6 +157,7 @@ struct WgradArgs {
   int nchunks;
   int64_t rows_per_chunk;
   int ntile_n, ntile_k;
+  int nset;  // steps in flight per workgroup: 4 (one workgroup per CU) or 2 (two)
 };
 void wgrad_plan(int64_t rows, int n, int k, int dtype, WgradArgs* a);
 int64_t wgrad_workspace_bytes(int64_t rows, int n, int k, int dtype);

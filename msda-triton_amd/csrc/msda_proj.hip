@@ -417,8 +417,8 @@ __global__ __launch_bounds__(kBlock) void transpose_kernel(const void* w0, const
 // (dispatch is round-robin over the 8 XCDs): the re-reads of each G and X
 // row segment by the chunk's other tiles then hit the same L2.
 // ---------------------------------------------------------------------------
-template <class T, bool MASKED, bool SPLITG>
-__global__ __launch_bounds__(kBlock) void wgrad_kernel(WgradArgs p) {
+template <class T, bool MASKED, bool SPLITG, int NSET>
+__global__ __launch_bounds__(kBlock, NSET == 2 ? 2 : 1) void wgrad_kernel(WgradArgs p) {
   constexpr int E = T::kBytes;
   constexpr int EPU = 16 / E;
   constexpr int UK = 2 * EPU;
@@ -475,10 +475,12 @@ __global__ __launch_bounds__(kBlock) void wgrad_kernel(WgradArgs p) {
   const uint32_t vx = xc < p.K ? rgo * ldx + (uint32_t)xc * E : kOob;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
 
-  // Four steps in flight (about 128 KB per workgroup): register sets 0..3
-  // rotate.  Masked rows are zeroed when parked: lane i < RW of a wave loads
-  // the mask byte of its share's row i, and a ballot turns them into bits.
-  constexpr int NSET = 4;
+  // NSET steps in flight per workgroup, register sets 0 .. NSET-1 rotating:
+  // four (~128 KB) when the launch has one workgroup per CU; two when it
+  // has more, which then fit two workgroups per CU (the registers of two
+  // waves per SIMD).  Masked rows are zeroed when parked: lane i < RW of a
+  // wave loads the mask byte of its share's row i, and a ballot turns them
+  // into bits.
   i32x4 gp[NSET][NI], xp[NSET][NI];
   uint32_t mk[NSET];
   auto load_step = [&](int sset, int64_t r0) {
@@ -769,19 +771,28 @@ hipError_t launch_proj_dtype(const ProjArgs& a, bool accumulate, hipStream_t st)
   }
 }
 
+template <class T, int NSET>
+void launch_wgrad_nset(const WgradArgs& a, int nblk, hipStream_t st) {
+  const bool m = a.mask != nullptr, sg = a.nsplit < a.N;
+  if (m && sg) {
+    hipLaunchKernelGGL((wgrad_kernel<T, true, true, NSET>), dim3(nblk), dim3(kBlock), 0, st, a);
+  } else if (m) {
+    hipLaunchKernelGGL((wgrad_kernel<T, true, false, NSET>), dim3(nblk), dim3(kBlock), 0, st, a);
+  } else if (sg) {
+    hipLaunchKernelGGL((wgrad_kernel<T, false, true, NSET>), dim3(nblk), dim3(kBlock), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((wgrad_kernel<T, false, false, NSET>), dim3(nblk), dim3(kBlock), 0, st, a);
+  }
+}
+
 template <class T>
 hipError_t launch_wgrad_t(WgradArgs a, void* dw0, void* dw1, void* db0, void* db1,
                           hipStream_t st) {
   const int nblk = a.nchunks * a.ntile_n * a.ntile_k;
-  const bool m = a.mask != nullptr, sg = a.nsplit < a.N;
-  if (m && sg) {
-    hipLaunchKernelGGL((wgrad_kernel<T, true, true>), dim3(nblk), dim3(kBlock), 0, st, a);
-  } else if (m) {
-    hipLaunchKernelGGL((wgrad_kernel<T, true, false>), dim3(nblk), dim3(kBlock), 0, st, a);
-  } else if (sg) {
-    hipLaunchKernelGGL((wgrad_kernel<T, false, true>), dim3(nblk), dim3(kBlock), 0, st, a);
+  if (a.nset == 4) {
+    launch_wgrad_nset<T, 4>(a, nblk, st);
   } else {
-    hipLaunchKernelGGL((wgrad_kernel<T, false, false>), dim3(nblk), dim3(kBlock), 0, st, a);
+    launch_wgrad_nset<T, 2>(a, nblk, st);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -858,19 +869,28 @@ void wgrad_plan(int64_t rows, int n, int k, int dtype, WgradArgs* a) {
   a->ntile_n = (n + 127) / 128;
   a->ntile_k = (k + 127) / 128;
   const int ntiles = a->ntile_n * a->ntile_k;
-  // About one workgroup per CU; chunk count a multiple of 8 (one group per XCD).
-  int want = cu_count() / ntiles;
+  // About two workgroups per CU; chunk count a multiple of 8 (one group per XCD).
+  int want = 2 * cu_count() / ntiles;
   if (want < 8) want = 8;
   int64_t steps = (rows + rs - 1) / rs;
   if (steps < 1) steps = 1;
   int64_t per = (steps + want - 1) / want;  // steps per chunk
-  per = (per + 3) / 4 * 4;                   // the kernel runs steps in fours
+  // At least four: short calls keep few chunks (a shorter partial reduction
+  // outweighs the longer chains there); a multiple of the steps in flight.
+  per = per < 4 ? 4 : (per + 1) / 2 * 2;
   // Buffer descriptors cover one chunk: keep its rows under 2^31 bytes.
   const int64_t row_bytes = (int64_t)(n > k ? n : k) * (dtype == kF32 ? 4 : 2);
   const int64_t max_steps = (((int64_t)1 << 31) - 1) / (row_bytes * rs) / 4 * 4;
   if (per > max_steps) per = max_steps > 4 ? max_steps : 4;
   int64_t chunks = (steps + per - 1) / per;
   chunks = (chunks + 7) / 8 * 8;
+  // One workgroup per CU or fewer: four steps in flight (per a multiple of 4).
+  a->nset = chunks * ntiles <= cu_count() ? 4 : 2;
+  if (a->nset == 4 && per % 4 != 0) {
+    per = (per + 3) / 4 * 4;
+    if (per > max_steps) per = max_steps;
+    chunks = ((steps + per - 1) / per + 7) / 8 * 8;
+  }
   a->rows_per_chunk = per * rs;
   a->nchunks = (int)chunks;
 }

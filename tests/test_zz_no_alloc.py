@@ -13,7 +13,7 @@ from msda_triton_amd import _native
 pytestmark = pytest.mark.gpu
 DEVICE = "cuda"
 DCODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
-SCRATCH_BYTES = 32 << 20
+SCRATCH_BYTES = 64 << 20
 
 
 def _inputs(rows, cin, n1, n2, dtype, seed):
@@ -75,16 +75,16 @@ def test_noalloc_projection_backward_matches_workspace_variant(dtype):
 
 
 def test_noalloc_projection_backward_refuses_beyond_its_scratch():
-    """fp32 1024 x 1024: a workspace over 32 MiB -> MSDA_ERR_UNSUPPORTED_SHAPE,
+    """fp32 2048 x 2048: a workspace over 64 MiB -> MSDA_ERR_UNSUPPORTED_SHAPE,
     returned before any launch (outputs untouched)."""
     lib = _native.load()
-    a = _inputs(10, 1024, 1024, 0, torch.float32, seed=3)
-    assert lib.msda_projection_workspace_bytes(10, 1024, 1024, 0) > SCRATCH_BYTES
-    gx = torch.full((10, 1024), 5.0, device=DEVICE)
+    a = _inputs(10, 2048, 2048, 0, torch.float32, seed=3)
+    assert lib.msda_projection_workspace_bytes(10, 2048, 2048, 0) > SCRATCH_BYTES
+    gx = torch.full((10, 2048), 5.0, device=DEVICE)
     p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     rc = lib.msda_projection_backward_noalloc(
         p(a["x"]), p(a["w1"]), None, p(a["mask"]), p(a["gy1"]), None, p(gx), None, None, None,
-        None, 10, 1024, 1024, 1024, 0, torch.cuda.current_stream().cuda_stream)
+        None, 10, 2048, 2048, 2048, 0, torch.cuda.current_stream().cuda_stream)
     assert rc == 3
     torch.cuda.synchronize()
     assert bool((gx == 5.0).all())
