@@ -128,7 +128,9 @@ constexpr int proj_waves_per_eu() {
   return NU == 16 ? 3 : 2;
 }
 
-template <class T, int NU, bool ACC, bool SPLITA, bool SPLITN>
+// WDIRECT: weights loaded straight into registers (launches with at most two
+// row blocks per workgroup) instead of through LDS.
+template <class T, int NU, bool ACC, bool SPLITA, bool SPLITN, bool WDIRECT>
 __global__ __launch_bounds__(kBlock)
 __attribute__((amdgpu_waves_per_eu(proj_waves_per_eu<NU, SPLITA>())))
 void proj_kernel(ProjArgs p) {
@@ -161,62 +163,88 @@ void proj_kernel(ProjArgs p) {
   const __amdgpu_buffer_rsrc_t ry1 = make_rsrc(SPLITN ? p.y1 : p.y0, SPLITN ? p.ybytes1 : 0u);
   const __amdgpu_buffer_rsrc_t rmask = make_rsrc(p.mask, p.mask != nullptr ? (uint32_t)p.rows : 0u);
 
-  // ---- weights -> registers: two passes of 64 weight rows through LDS ----
-  // Loads are coalesced row chunks; for NU == 16 both passes' loads are issued
-  // before the first LDS pass (one memory latency for the whole prologue).
+  // ---- weights -> registers ----
   const int colw = blockIdx.y * 128;  // first output column of this workgroup
   const int col0 = colw + wave * 32;  // ... of this wave
-  constexpr int WQ = 2 * ROUNDS;      // loads per thread per pass
-  auto wload = [&](int pass, int q) {
-    const int idx = tid + kBlock * q;
-    const int r = idx / CPR;  // 0..63
-    const int ch = idx - r * CPR;
-    const int c = colw + pass * 64 + r;
-    const int k = ch * EPU;
-    i32x4 v = i32x4{0, 0, 0, 0};
-    if (c < p.N && k < p.K) {
-      const bool hi = c >= p.nsplit;
-      const char* base = static_cast<const char*>(hi ? p.w1 : p.w0);
-      v = ld16(base + ((int64_t)(hi ? c - p.nsplit : c) * p.ldw + k) * E);
-    }
-    return v;
-  };
-  auto wpark = [&](int q, const i32x4& v) {
-    const int idx = tid + kBlock * q;
-    const int r = idx / CPR;
-    const int ch = idx - r * CPR;
-    *reinterpret_cast<i32x4*>(smem + r * ROWB + swz(r, ch) * 16) = v;
-  };
   i32x4 w[NU];
-  auto wpick = [&](int pass) {
-    __syncthreads();
-    if ((wave >> 1) == pass) {
-      const int r = (wave & 1) * 32 + rl;
+  if constexpr (WDIRECT) {
+    // Lane (rl, slot) of a wave holds, for its output column c = col0 + rl,
+    // the 16-byte pieces 2u + slot (u < NU) of weight row c: loaded straight
+    // into the MFMA operand layout, all NU loads in flight (one memory latency,
+    // no LDS passes or barriers; the weights are L2-resident after the first
+    // workgroups).  Buffer range checks give zeros past N and past K.
+    {
+      const int c = col0 + rl;
+      const bool hi = c >= p.nsplit;
+      const int cr = hi ? c - p.nsplit : c;  // row within its weight
+      const int nw = hi ? p.N - p.nsplit : p.nsplit;
+      const __amdgpu_buffer_rsrc_t rw =
+          make_rsrc(hi ? p.w1 : p.w0, (uint32_t)((int64_t)nw * p.ldw * E));
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
-        w[u] = *reinterpret_cast<const i32x4*>(smem + r * ROWB + swz(r, 2 * u + slot) * 16);
+        const int k = (2 * u + slot) * EPU;
+        const uint32_t off = (c < p.N && k < p.K) ? (uint32_t)(((int64_t)cr * p.ldw + k) * E) : kOob;
+        w[u] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
       }
     }
-    __syncthreads();
-  };
-  if constexpr (NU == 16) {
-    i32x4 st0[WQ], st1[WQ];
-#pragma unroll
-    for (int q = 0; q < WQ; ++q) st0[q] = wload(0, q);
-#pragma unroll
-    for (int q = 0; q < WQ; ++q) st1[q] = wload(1, q);
-#pragma unroll
-    for (int q = 0; q < WQ; ++q) wpark(q, st0[q]);
-    wpick(0);
-#pragma unroll
-    for (int q = 0; q < WQ; ++q) wpark(q, st1[q]);
-    wpick(1);
   } else {
+    // Two passes of 64 weight rows through LDS, loaded as coalesced row
+    // chunks (for NU == 16 both passes' loads are issued before the first
+    // LDS pass: one memory latency for the whole prologue).  Used by the
+    // launches with several row blocks per workgroup: there hundreds of
+    // workgroups start at once, and the direct path's scattered 32-byte
+    // weight reads slowed the value projection's forward (24.8 -> 27.3 us).
+    constexpr int WQ = 2 * ROUNDS;      // loads per thread per pass
+    auto wload = [&](int pass, int q) {
+      const int idx = tid + kBlock * q;
+      const int r = idx / CPR;  // 0..63
+      const int ch = idx - r * CPR;
+      const int c = colw + pass * 64 + r;
+      const int k = ch * EPU;
+      i32x4 v = i32x4{0, 0, 0, 0};
+      if (c < p.N && k < p.K) {
+        const bool hi = c >= p.nsplit;
+        const char* base = static_cast<const char*>(hi ? p.w1 : p.w0);
+        v = ld16(base + ((int64_t)(hi ? c - p.nsplit : c) * p.ldw + k) * E);
+      }
+      return v;
+    };
+    auto wpark = [&](int q, const i32x4& v) {
+      const int idx = tid + kBlock * q;
+      const int r = idx / CPR;
+      const int ch = idx - r * CPR;
+      *reinterpret_cast<i32x4*>(smem + r * ROWB + swz(r, ch) * 16) = v;
+    };
+    auto wpick = [&](int pass) {
+      __syncthreads();
+      if ((wave >> 1) == pass) {
+        const int r = (wave & 1) * 32 + rl;
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
+        for (int u = 0; u < NU; ++u) {
+          w[u] = *reinterpret_cast<const i32x4*>(smem + r * ROWB + swz(r, 2 * u + slot) * 16);
+        }
+      }
+      __syncthreads();
+    };
+    if constexpr (NU == 16) {
+      i32x4 st0[WQ], st1[WQ];
 #pragma unroll
-      for (int q = 0; q < WQ; ++q) wpark(q, wload(pass, q));
-      wpick(pass);
+      for (int q = 0; q < WQ; ++q) st0[q] = wload(0, q);
+#pragma unroll
+      for (int q = 0; q < WQ; ++q) st1[q] = wload(1, q);
+#pragma unroll
+      for (int q = 0; q < WQ; ++q) wpark(q, st0[q]);
+      wpick(0);
+#pragma unroll
+      for (int q = 0; q < WQ; ++q) wpark(q, st1[q]);
+      wpick(1);
+    } else {
+#pragma unroll
+      for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+        for (int q = 0; q < WQ; ++q) wpark(q, wload(pass, q));
+        wpick(pass);
+      }
     }
   }
   const int c_lane = col0 + rl;
@@ -747,8 +775,13 @@ hipError_t launch_proj_t(ProjArgs a, hipStream_t st) {
   const int per = (a.nblocks + want - 1) / want;
   int gx = (a.nblocks + per - 1) / per;
   gx = (gx + 7) / 8 * 8;
-  hipLaunchKernelGGL((proj_kernel<T, NU, ACC, SPLITA, SPLITN>), dim3(gx, gy), dim3(kBlock), 0, st,
-                     a);
+  if (per <= 2) {
+    hipLaunchKernelGGL((proj_kernel<T, NU, ACC, SPLITA, SPLITN, true>), dim3(gx, gy), dim3(kBlock),
+                       0, st, a);
+  } else {
+    hipLaunchKernelGGL((proj_kernel<T, NU, ACC, SPLITA, SPLITN, false>), dim3(gx, gy), dim3(kBlock),
+                       0, st, a);
+  }
   return hipGetLastError();
 }
 
