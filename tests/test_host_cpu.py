@@ -343,6 +343,23 @@ def test_projection_backward_argument_errors(lib):
     assert lib.msda_projection_workspace_bytes(100, 256, 256, 9) == -1
 
 
+def test_projection_workspace_fits_the_noalloc_scratch():
+    """msda_projection_backward_noalloc's scratch (64 MiB) holds the workspace
+    (transposed weight + per-chunk weight-gradient partials) of every
+    half-precision projection the library takes -- reductions of at most 512
+    -- and of fp32 ones up to 512 x 512, at any row count (the chunk count is
+    bounded by the CU count: 256 on MI355X, also the host-side default)."""
+    lib = _native.load()
+    limit = 64 << 20
+    for dtype, feats in ((1, (16, 64, 128, 256, 384, 512)), (2, (16, 64, 128, 256, 384, 512)),
+                         (0, (16, 64, 256, 512))):
+        for cin in feats:
+            for out in feats:
+                for rows in (1, 1200, 88892, 10 ** 6, 10 ** 7):
+                    need = lib.msda_projection_workspace_bytes(rows, cin, out, dtype)
+                    assert 0 < need <= limit, (rows, cin, out, dtype, need)
+
+
 def test_projection_rejects_cpu_tensors():
     from msda_triton_amd.projection import projection
 
