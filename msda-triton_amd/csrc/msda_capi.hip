@@ -657,6 +657,10 @@ static std::mutex g_side_mu;
 static SideStream* side_stream_locked(hipStream_t caller) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kSideMaxDevices) return nullptr;
+  // The caller's stream must belong to the current device (the side stream
+  // is that device's); otherwise the call runs on the caller's stream alone.
+  hipDevice_t sdev = -1;
+  if (hipStreamGetDevice(caller, &sdev) != hipSuccess || sdev != dev) return nullptr;
   SideStream& ss = g_side[dev];
   if (!ss.s) {
     // Not created under graph capture (creation may be illegal there): a
