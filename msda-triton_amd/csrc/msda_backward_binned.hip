@@ -97,23 +97,28 @@ __device__ __forceinline__ BinSrc bin_src(const Params& p, const BinArgs& a) {
                 make_rsrc(p.ref, p.ref_bytes), make_rsrc(p.lse, (uint32_t)p.npairs * 4u)};
 }
 
+// `dead` (0 or 0x80000000) is OR-ed into the byte offset: a dead lane's
+// load lies past num_records (< 2^31) and reads zeros, so callers issue the
+// loads without a branch (a branch whose block also uses the value makes the
+// compiler wait for each load before the next is issued).
 template <class T>
-__device__ __forceinline__ void bin_xy(__amdgpu_buffer_rsrc_t r, uint32_t i, float& x, float& y) {
+__device__ __forceinline__ void bin_xy(__amdgpu_buffer_rsrc_t r, uint32_t i, float& x, float& y,
+                                       uint32_t dead = 0u) {
   if constexpr (T::kBytes == 4) {
-    const i32x2 xy = __builtin_amdgcn_raw_buffer_load_b64(r, i * 8u, 0, 0);
+    const i32x2 xy = __builtin_amdgcn_raw_buffer_load_b64(r, (i * 8u) | dead, 0, 0);
     x = __int_as_float(xy[0]);
     y = __int_as_float(xy[1]);
   } else {
-    unpack2<T>((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, 0), x, y);
+    unpack2<T>((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (i * 4u) | dead, 0, 0), x, y);
   }
 }
 
 template <class T>
-__device__ __forceinline__ float bin_one(__amdgpu_buffer_rsrc_t r, uint32_t i) {
+__device__ __forceinline__ float bin_one(__amdgpu_buffer_rsrc_t r, uint32_t i, uint32_t dead = 0u) {
   if constexpr (T::kBytes == 4) {
-    return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, 0));
+    return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (i * 4u) | dead, 0, 0));
   } else {
-    return unpack1<T>((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, i * 2u, 0, 0));
+    return unpack1<T>((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (i * 2u) | dead, 0, 0));
   }
 }
 
@@ -125,15 +130,17 @@ struct BinIn {
 
 template <class T, bool FUSED, bool kWeight>
 __device__ __forceinline__ BinIn bin_load(const Params& p, const BinSrc& rs, uint32_t bq,
-                                          uint32_t pair, uint32_t pi, uint32_t l) {
+                                          uint32_t pair, uint32_t pi, uint32_t l,
+                                          uint32_t dead = 0u) {
   BinIn r;
-  bin_xy<T>(rs.loc, pi, r.x, r.y);
-  r.a = kWeight ? bin_one<T>(rs.attn, pi) : 0.f;
+  bin_xy<T>(rs.loc, pi, r.x, r.y, dead);
+  r.a = kWeight ? bin_one<T>(rs.attn, pi, dead) : 0.f;
   r.rx = r.ry = r.lse = 0.f;
   if constexpr (FUSED) {
-    bin_xy<T>(rs.ref, p.ref_levels ? bq * (uint32_t)p.L + l : bq, r.rx, r.ry);
+    bin_xy<T>(rs.ref, p.ref_levels ? bq * (uint32_t)p.L + l : bq, r.rx, r.ry, dead);
     if constexpr (kWeight)
-      r.lse = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs.lse, pair * 4u, 0, 0));
+      r.lse = __int_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(rs.lse, (pair * 4u) | dead, 0, 0));
   }
   return r;
 }
@@ -191,16 +198,15 @@ __device__ __forceinline__ void bin_keys(const Params& p, const BinArgs& a, cons
                        (threadIdx.x & (kWave - 1));
   BinIn in[kBinIt];
 #pragma unroll
-  for (int u = 0; u < kBinIt; ++u) {  // all loads in flight together
+  for (int u = 0; u < kBinIt; ++u) {  // all loads in flight together (no branch)
     const uint32_t li = li0 + u * kWave;
-    in[u] = BinIn{0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (li < qk) {
-      const uint32_t q = fdiv(li, p.div_k), k = li - q * (uint32_t)p.K;
-      const uint32_t bq = (uint32_t)gl.b * p.Q + q;
-      const uint32_t pair = bq * p.M + gl.m;
-      const uint32_t pi = pair * (uint32_t)p.LK + (uint32_t)gl.l * p.K + k;
-      in[u] = bin_load<T, FUSED, false>(p, rs, bq, pair, pi, gl.l);
-    }
+    const bool ok = li < qk;
+    const uint32_t lc = ok ? li : 0u;
+    const uint32_t q = fdiv(lc, p.div_k), k = lc - q * (uint32_t)p.K;
+    const uint32_t bq = (uint32_t)gl.b * p.Q + q;
+    const uint32_t pair = bq * p.M + gl.m;
+    const uint32_t pi = pair * (uint32_t)p.LK + (uint32_t)gl.l * p.K + k;
+    in[u] = bin_load<T, FUSED, false>(p, rs, bq, pair, pi, gl.l, ok ? 0u : 0x80000000u);
   }
 #pragma unroll
   for (int u = 0; u < kBinIt; ++u) {
@@ -278,9 +284,32 @@ __global__ __launch_bounds__(kBlock) void bin_fill_kernel(Params p, BinArgs a) {
 #pragma unroll
   for (int w = 0; w < kBlock / kWave; ++w)
     for (int j = threadIdx.x; j < nwd; j += kBlock) s_cnt[w][j] = 0u;
-  const uint32_t* const row = a.mat + ((uint64_t)g * a.nqb + qb) * a.nbmax;
-  const uint32_t* const cur = a.cursors + (uint32_t)g * a.nbmax;
-  for (int j = threadIdx.x; j < gl.nk; j += kBlock) s_base[j] = cur[j] + row[j];
+  // Every key's base: its cursor + its entries in earlier blocks.  All loads
+  // issued before the first is used (buffer loads: past the last key they
+  // read zeros); a loop that stored each pair before loading the next waited
+  // out one memory round trip per 256 keys.
+  {
+    const __amdgpu_buffer_rsrc_t rrow = make_rsrc(
+        a.mat + ((uint64_t)g * a.nqb + qb) * a.nbmax, (uint32_t)gl.nk * 4u);
+    const __amdgpu_buffer_rsrc_t rcur = make_rsrc(a.cursors + (uint32_t)g * a.nbmax,
+                                                  (uint32_t)gl.nk * 4u);
+    constexpr int kIt = kBinMaxBands / kBlock;
+    uint32_t v[kIt];
+#pragma unroll
+    for (int i = 0; i < kIt; ++i) {
+      const uint32_t o = (uint32_t)(threadIdx.x + i * kBlock) * 4u;
+      v[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rcur, o, 0, 0) +
+             (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rrow, o, 0, 0);
+    }
+    // (The compiler would sink each load into its guarded store below.)
+#pragma unroll
+    for (int i = 0; i < kIt; ++i) asm volatile("" : "+v"(v[i]));
+#pragma unroll
+    for (int i = 0; i < kIt; ++i) {
+      const int j = threadIdx.x + i * kBlock;
+      if (j < gl.nk) s_base[j] = v[i];
+    }
+  }
   __syncthreads();
   uint32_t key[kBinIt], rank[kBinIt];
   bin_keys<T, FUSED>(p, a, gl, qb, key);
