@@ -955,15 +955,7 @@ bool owner_plan(int64_t B, int64_t Q, int64_t K, int64_t D, int64_t S, int64_t L
     *full = wgs(s) >= want;
     return s;
   };
-  // Calls with five sample slots per lane on the 19 KB build (Q K in
-  // 1025..1280: DETR's 300 queries x 4 points) take 1536-row bands:
-  // high-contention 41.6 -> 37.7 us, decoder fp16 20.8 -> 20.5, decoder bf16
-  // unchanged (21.2; same-process alternating A/B after a warm-up call).
-  // Other shapes measured mixed (Q K = 400..2000, B = 1..8), so they keep
-  // kOwnRows.
-  const int64_t ns5 = (Q * K + kBlock - 1) / kBlock;
-  const int64_t rows_dflt = (!big && ns5 == 5) ? kOwnRows * 3 / 4 : kOwnRows;
-  int64_t rows = own_knob(MSDA_KNOB_OWN_ROWS, rows_dflt, 64, kOwnRows);
+  int64_t rows = own_knob(MSDA_KNOB_OWN_ROWS, kOwnRows, 64, kOwnRows);
   bool full = true;
   int64_t split = plan_split(rows, &full);
   if (!full && !launch_override_set(MSDA_KNOB_OWN_ROWS)) {
