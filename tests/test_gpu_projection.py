@@ -243,3 +243,28 @@ def test_projection_backward_second_stream_graph_replays(case):
         torch.cuda.synchronize()
         for k, v in eager.items():
             assert torch.equal(outs_g[k], v), f"replay {rep}: {k} differs from the eager call"
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_projection_weight_paths_agree_bitwise(dtype):
+    """Launches with at most two 32-row blocks per workgroup load the weights
+    straight into registers, larger ones through LDS; both feed the same MFMA
+    operands, and each output row depends on its input row alone.  So the
+    first 1,200 rows of a 30,000-row call (LDS path) equal a 1,200-row call
+    on those rows (direct path) bit for bit, with the weight split in two and
+    masked rows."""
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(30000, 256, generator=g).to(DEVICE, dtype)
+    w = (torch.randn(256, 256, generator=g) / 16).to(DEVICE, dtype)
+    b = torch.randn(256, generator=g).to(DEVICE, dtype)
+    w2 = (torch.randn(128, 256, generator=g) / 16).to(DEVICE, dtype)
+    b2 = torch.randn(128, generator=g).to(DEVICE, dtype)
+    mask = (torch.rand(30000, generator=g) < 0.1).to(DEVICE)
+    big = projection(x, w, b, row_mask=mask, weight2=w2, bias2=b2)
+    small = projection(x[:1200], w, b, row_mask=mask[:1200], weight2=w2, bias2=b2)
+    for yb, ys in zip(big, small):
+        assert torch.equal(yb[:1200], ys)
+    ref = projection_reference(np64(x[:1200]), np64(w), np64(b), np64(mask[:1200]).astype(bool),
+                               np64(w2), np64(b2))
+    for ys, r in zip(small, ref):
+        assert rel_err(ys, torch.from_numpy(r)) <= FWD_RELERR[dtype]
