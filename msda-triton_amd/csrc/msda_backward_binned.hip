@@ -145,21 +145,30 @@ __device__ __forceinline__ BinIn bin_load(const Params& p, const BinSrc& rs, uin
   return r;
 }
 
-// Exclusive prefix sum over the workgroup (Hillis-Steele in `s`); `total`
-// receives the sum.  Every thread must call it.
+// Exclusive prefix sum over the workgroup; `total` receives the sum.  A
+// shuffle scan within each wave, then the waves' totals through `s` (one
+// barrier, and one more so that `s` can be reused by the next call).  Every
+// thread must call it.
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* s, uint32_t& total) {
-  s[threadIdx.x] = v;
-  __syncthreads();
-  for (int d = 1; d < kBlock; d <<= 1) {
-    const uint32_t x = (int)threadIdx.x >= d ? s[threadIdx.x - d] : 0u;
-    __syncthreads();
-    s[threadIdx.x] += x;
-    __syncthreads();
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  uint32_t x = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t y = __shfl_up(x, d);
+    if (lane >= d) x += y;
   }
-  total = s[kBlock - 1];
-  const uint32_t incl = s[threadIdx.x];
+  if (lane == kWave - 1) s[wave] = x;
   __syncthreads();
-  return incl - v;
+  uint32_t base = 0u, tot = 0u;
+#pragma unroll
+  for (int w = 0; w < kBlock / kWave; ++w) {
+    const uint32_t t = s[w];
+    base += w < wave ? t : 0u;
+    tot += t;
+  }
+  total = tot;
+  __syncthreads();
+  return base + x - v;
 }
 
 struct GroupLevel {
