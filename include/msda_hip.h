@@ -258,8 +258,9 @@ int msda_projection_forward(const void* input, const void* weight, const void* b
                             void* output, void* output2, int64_t rows, int64_t in_features,
                             int64_t out_features, int64_t split, int dtype, void* stream);
 
-/* Bytes of the fp32 workspace msda_projection_backward needs for weight and
- * bias gradients (-1 for invalid arguments). */
+/* Bytes of the workspace msda_projection_backward needs (the transposed
+ * weights and the weight / bias gradients' fp32 partial sums; -1 for invalid
+ * arguments). */
 int64_t msda_projection_workspace_bytes(int64_t rows, int64_t in_features, int64_t out_features,
                                         int dtype);
 
@@ -270,9 +271,10 @@ int64_t msda_projection_workspace_bytes(int64_t rows, int64_t in_features, int64
  *   grad_input   = [grad_output | grad_output2] [weight ; weight2], masked rows 0
  *   grad_weight  = grad_output^T input over unmasked rows, grad_weight2 likewise
  *   grad_bias    = column sums of grad_output over unmasked rows, grad_bias2 likewise
- * Weight / bias gradients need `workspace` (msda_projection_workspace_bytes,
- * 16-byte aligned, contents ignored); they are fixed-order sums (no atomics),
- * so every output is bitwise reproducible.  When grad_input and a weight or
+ * Every gradient, grad_input included, needs `workspace`
+ * (msda_projection_workspace_bytes, 16-byte aligned, contents ignored; NULL
+ * only when no gradient is asked for or rows == 0).  Weight / bias gradients
+ * are fixed-order sums (no atomics), so every output is bitwise reproducible.  When grad_input and a weight or
  * bias gradient are both asked for, the weight/bias half runs on a second
  * stream of the library's (one per device, default priority, created on the
  * first such call), forked from and joined back into `stream` with events:

@@ -257,34 +257,34 @@ void proj_kernel(ProjArgs p) {
 
   // ---- activation blocks ----
   // Rows are clamped to nrows, whose offsets lie at or past num_records.
-  i32x4 pre[SPLITA ? ROUNDS : 1];
+  // Each lane's 16-byte piece goes HBM -> LDS directly (its LDS slot is fixed
+  // by the lane id).  With a split input the lanes pick their source by a
+  // branch: the two loads run under complementary EXEC masks, and a masked
+  // lane neither fetches nor writes LDS (no staging registers: loading both
+  // sources into registers and merging them held two 16-byte results per
+  // piece in flight and spilled the weight registers).
   uint32_t pre_mask = 0u;
   auto issue_block = [&](int pb, int blk) {
     const int r0 = blk * 32;
     unsigned char* b = smem + pb * BUFB;
-    if constexpr (!SPLITA) {
 #pragma unroll
-      for (int j = 0; j < IPW; ++j) {
-        const int byte = (wave * IPW + j) * 1024 + lane * 16;
-        const int r = byte / ROWB;
-        const int c = swz(r, (byte - r * ROWB) / 16);
-        const int k = c * EPU;
-        const uint32_t row = (uint32_t)min(r0 + r, nrows);
+    for (int j = 0; j < IPW; ++j) {
+      const int byte = (wave * IPW + j) * 1024 + lane * 16;
+      const int r = byte / ROWB;
+      const int c = swz(r, (byte - r * ROWB) / 16);
+      const int k = c * EPU;
+      const uint32_t row = (uint32_t)min(r0 + r, nrows);
+      unsigned char* dst = b + (wave * IPW + j) * 1024;
+      if constexpr (!SPLITA) {
         const uint32_t off = k < p.K ? (row * lda0 + k) * E : kOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra0, b + (wave * IPW + j) * 1024, 16, off, 0, 0,
-                                                 0);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < ROUNDS; ++q) {
-        const int idx = tid + kBlock * q;
-        const int r = idx / CPR;
-        const int k = (idx - r * CPR) * EPU;
-        const uint32_t row = (uint32_t)min(r0 + r, nrows);
-        const uint32_t o0 = k < p.ksplit ? (row * lda0 + k) * E : kOob;
-        const uint32_t o1 = (k >= p.ksplit && k < p.K) ? (row * lda1 + k - p.ksplit) * E : kOob;
-        pre[q] = __builtin_amdgcn_raw_buffer_load_b128(ra0, o0, 0, 0) |
-                 __builtin_amdgcn_raw_buffer_load_b128(ra1, o1, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra0, dst, 16, off, 0, 0, 0);
+      } else {
+        if (k < p.ksplit) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(ra0, dst, 16, (row * lda0 + k) * E, 0, 0, 0);
+        } else {
+          const uint32_t off = k < p.K ? (row * lda1 + k - p.ksplit) * E : kOob;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(ra1, dst, 16, off, 0, 0, 0);
+        }
       }
     }
     pre_mask = (wave == 0 && lane < 32)
@@ -292,20 +292,6 @@ void proj_kernel(ProjArgs p) {
                          rmask, (uint32_t)min(r0 + lane, nrows), 0, 0)
                    : 0u;
   };
-  // SPLITA only: registers -> LDS (swizzled), before the block's barrier.
-  auto park_block = [&](int pb) {
-    if constexpr (SPLITA) {
-      unsigned char* b = smem + pb * BUFB;
-#pragma unroll
-      for (int q = 0; q < ROUNDS; ++q) {
-        const int idx = tid + kBlock * q;
-        const int r = idx / CPR;
-        const int ch = idx - r * CPR;
-        *reinterpret_cast<i32x4*>(b + r * ROWB + swz(r, ch) * 16) = pre[q];
-      }
-    }
-  };
-
   const int blk0 = blockIdx.x;
   issue_block(0, blk0);
   int pb = 0;
@@ -313,7 +299,6 @@ void proj_kernel(ProjArgs p) {
   // refilled (issue_block) right after the barrier of block j, which every
   // wave passes only after finishing block j-1, the buffer's previous reader.
   for (int blk = blk0; blk < p.nblocks; blk += gridDim.x) {
-    park_block(pb);
     if (wave == 0) {
       const uint64_t bits = __ballot(pre_mask != 0u);
       if (lane == 0) smask[pb] = (uint32_t)bits;

@@ -108,7 +108,8 @@ class _ProjectionFunction(torch.autograd.Function):
         gb2 = torch.empty(n2, dtype=x.dtype, device=x.device) if need_b2 else None
         lib = _native.load()
         ws = None
-        if need_w or need_b or need_w2 or need_b2:
+        # grad_input needs the workspace too (it holds the transposed weights).
+        if (need_x and rows > 0) or need_w or need_b or need_w2 or need_b2:
             nbytes = lib.msda_projection_workspace_bytes(rows, x.shape[-1], n1 + n2, dt)
             if nbytes < 0:
                 raise RuntimeError("msda_projection_workspace_bytes rejected the shape")

@@ -268,3 +268,36 @@ def test_projection_weight_paths_agree_bitwise(dtype):
                                np64(w2), np64(b2))
     for ys, r in zip(small, ref):
         assert rel_err(ys, torch.from_numpy(r)) <= FWD_RELERR[dtype]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_projection_split_input_paths_agree_bitwise(dtype):
+    """grad_input of a split call reads its reduction from two tensors
+    (grad_output and grad_output2), picked per 16-byte piece.  Row r of it
+    depends on row r of those alone, so the first 1,200 rows of a 30,000-row
+    backward (weights through LDS) equal a 1,200-row backward on those rows
+    (weights straight into registers) bit for bit, and the small call meets
+    the oracle; masked rows get zeros."""
+    g = torch.Generator().manual_seed(22)
+    x = torch.randn(30000, 256, generator=g).to(DEVICE, dtype)
+    w = (torch.randn(256, 256, generator=g) / 16).to(DEVICE, dtype)
+    b = torch.randn(256, generator=g).to(DEVICE, dtype)
+    w2 = (torch.randn(128, 256, generator=g) / 16).to(DEVICE, dtype)
+    b2 = torch.randn(128, generator=g).to(DEVICE, dtype)
+    mask = (torch.rand(30000, generator=g) < 0.1).to(DEVICE)
+    gy = torch.randn(30000, 256, generator=g).to(DEVICE, dtype)
+    gy2 = torch.randn(30000, 128, generator=g).to(DEVICE, dtype)
+
+    def grad_input(n):
+        xi = x[:n].clone().requires_grad_(True)
+        outs = projection(xi, w, b, row_mask=mask[:n], weight2=w2, bias2=b2)
+        torch.autograd.backward(outs, [gy[:n], gy2[:n]])
+        return xi.grad
+
+    big, small = grad_input(30000), grad_input(1200)
+    assert torch.equal(big[:1200], small)
+    assert not big[mask].any(), "masked rows get zero input gradient"
+    ref = projection_backward_reference(np64(x[:1200]), np64(w), np64(gy[:1200]),
+                                        np64(mask[:1200]).astype(bool), np64(w2),
+                                        np64(gy2[:1200]))
+    assert rel_err(small, torch.from_numpy(ref[0])) <= BWD_RELERR[dtype]
