@@ -893,17 +893,19 @@ void wgrad_plan(int64_t rows, int n, int k, int dtype, WgradArgs* a) {
   int64_t steps = (rows + rs - 1) / rs;
   if (steps < 1) steps = 1;
   int64_t per = (steps + want - 1) / want;  // steps per chunk
-  // At least four: short calls keep few chunks (a shorter partial reduction
-  // outweighs the longer chains there); a multiple of the steps in flight.
-  per = per < 4 ? 4 : (per + 1) / 2 * 2;
+  // At least two steps: short calls keep few chunks (one-step chunks made
+  // the partial reduction longer than the chains they saved); a multiple of
+  // the steps in flight.
+  per = per < 2 ? 2 : (per + 1) / 2 * 2;
   // Buffer descriptors cover one chunk: keep its rows under 2^31 bytes.
   const int64_t row_bytes = (int64_t)(n > k ? n : k) * (dtype == kF32 ? 4 : 2);
   const int64_t max_steps = (((int64_t)1 << 31) - 1) / (row_bytes * rs) / 4 * 4;
   if (per > max_steps) per = max_steps > 4 ? max_steps : 4;
   int64_t chunks = (steps + per - 1) / per;
   chunks = (chunks + 7) / 8 * 8;
-  // One workgroup per CU or fewer: four steps in flight (per a multiple of 4).
-  a->nset = chunks * ntiles <= cu_count() ? 4 : 2;
+  // One workgroup per CU or fewer and chunks of four steps or more: four
+  // steps in flight (per a multiple of 4).
+  a->nset = (chunks * ntiles <= cu_count() && per >= 4) ? 4 : 2;
   if (a->nset == 4 && per % 4 != 0) {
     per = (per + 3) / 4 * 4;
     if (per > max_steps) per = max_steps;
