@@ -260,9 +260,22 @@ __global__ __launch_bounds__(kBlock) void bin_count_kernel(Params p, BinArgs a) 
   __syncthreads();
   uint32_t key[kBinIt];
   bin_keys<T, FUSED>(p, a, gl, qb, key);
+  // Neighbouring lanes hold neighbouring samples (a query's K points, then
+  // the next query's), which mostly share a key: each run of equal keys in
+  // a wave instruction adds its length once, from its first lane (lanes
+  // adding to one LDS word in one instruction are serialised).
+  const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
-  for (int u = 0; u < kBinIt; ++u)
-    if (key[u] != ~0u) atomicAdd(&s_hist[key[u]], 1u);
+  for (int u = 0; u < kBinIt; ++u) {
+    const uint32_t k = key[u];
+    // wave_shr:1 -- lane i receives lane i - 1's key; lane 0 keeps ~k.
+    const uint32_t prev = __builtin_amdgcn_update_dpp(~k, k, 0x138, 0xF, 0xF, false);
+    const bool head = prev != k;
+    const uint64_t hm = __ballot(head);
+    const uint64_t above = lane == kWave - 1 ? 0ull : hm >> (lane + 1);
+    const int next = above ? lane + 1 + __builtin_ctzll(above) : kWave;
+    if (head && k != ~0u) atomicAdd(&s_hist[k], (uint32_t)(next - lane));
+  }
   __syncthreads();
   uint32_t* const row = a.mat + ((uint64_t)g * a.nqb + qb) * a.nbmax;
   for (int j = threadIdx.x; j < gl.nk; j += kBlock) row[j] = s_hist[j];
