@@ -239,10 +239,36 @@ void proj_kernel(ProjArgs p) {
       for (int q = 0; q < WQ; ++q) wpark(q, st1[q]);
       wpick(1);
     } else {
+      // NU == 32: a weight row is 1 KB, one wave instruction's worth of
+      // 16-byte pieces, so each pass goes HBM -> LDS directly (lane `lane`
+      // of the instruction for LDS row r fills position `lane`, i.e. chunk
+      // swz(r, lane)); staging the pass in registers held 64 VGPRs beside
+      // the 128 weight registers and spilled.
+      static_assert(ROWB == kWave * 16, "one weight row per wave instruction");
+      const __amdgpu_buffer_rsrc_t rw0 =
+          make_rsrc(p.w0, (uint32_t)((int64_t)p.nsplit * p.ldw * E));
+      const __amdgpu_buffer_rsrc_t rw1 =
+          make_rsrc(p.w1 != nullptr ? p.w1 : p.w0,
+                    p.w1 != nullptr ? (uint32_t)((int64_t)(p.N - p.nsplit) * p.ldw * E) : 0u);
 #pragma unroll
       for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
-        for (int q = 0; q < WQ; ++q) wpark(q, wload(pass, q));
+        for (int j = 0; j < 64 / (kBlock / kWave); ++j) {
+          const int r = wave * (64 / (kBlock / kWave)) + j;  // LDS row
+          const int c = colw + pass * 64 + r;                // weight row
+          const int kk = swz(r, lane) * EPU;
+          const bool hi = c >= p.nsplit;
+          const int cr = hi ? c - p.nsplit : c;
+          const uint32_t off =
+              (c < p.N && kk < p.K) ? (uint32_t)(((int64_t)cr * p.ldw + kk) * E) : kOob;
+          unsigned char* dst = smem + r * ROWB;
+          if (hi) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw1, dst, 16, off, 0, 0, 0);
+          } else {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw0, dst, 16, off, 0, 0, 0);
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this pass's rows have landed in LDS
         wpick(pass);
       }
     }
