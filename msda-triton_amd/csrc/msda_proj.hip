@@ -695,7 +695,13 @@ __global__ __launch_bounds__(kBlock) void wgrad_reduce_kernel(WgradArgs p, void*
   for (int64_t base = (int64_t)blockIdx.x * 64; base < total; base += (int64_t)gridDim.x * 64) {
     const int64_t i0 = base + 4 * g;  // this lane's 4 outputs: i0 .. i0+3
     float4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (base + 64 <= nk && (nk & 3) == 0) {
+    if (base + 64 <= nk && (nk & 3) == 0 && nper == 1) {
+      // At most 16 chunks: one partial per lane (cs), none past the end.
+      if (cs < p.nchunks) {
+        const float4 v = *reinterpret_cast<const float4*>(p.ws + (int64_t)cs * nk + i0);
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+      }
+    } else if (base + 64 <= nk && (nk & 3) == 0) {
       for (int j0 = 0; j0 < nper; j0 += 4) {
         float4 v[4];
 #pragma unroll
